@@ -1,0 +1,32 @@
+"""MI355X-native U4 MoE expert hot path (batch-1 decode + grouped prefill).
+
+Hand-written HIP kernels for gfx950 in ``csrc/`` are built into
+``libaima_u4moe.so`` behind the C ABI of ``include/aima_u4moe.h``; this
+package is the thin host layer over it.  The package directory name is not a
+Python identifier, so it is imported under the name ``aima_u4moe``
+(``__graft_entry__.load_package()`` registers it).
+"""
+
+from . import _lib, layout, ops, runtime, synth  # noqa: F401
+from ._lib import AimaError  # noqa: F401
+from .layout import MoeLayerWeights, U4Weight  # noqa: F401
+from .ops import (  # noqa: F401
+    MIN_WEIGHT_SUM,
+    Workspace,
+    apply_rms_norm,
+    build_grouped_schedule,
+    grouped_moe_prefill,
+    matvec_u4,
+    moe_decode_down,
+    moe_decode_gate_up,
+    moe_stack_decode,
+    moe_stack_prefill,
+    run_moe_ffn_layer,
+    select_router_topk,
+    u4_dequant,
+)
+from .runtime import (  # noqa: F401
+    GroupedU4PrefillInput,
+    GroupedU4PrefillRun,
+    GroupedU4PrefillRuntime,
+)

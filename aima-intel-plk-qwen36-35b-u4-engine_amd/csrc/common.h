@@ -1,0 +1,171 @@
+// Shared device helpers for the gfx950 U4 MoE kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "aima_u4moe.h"
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+namespace aima {
+
+// ---------------------------------------------------------------------------
+// host-side error state (thread-local message behind aima_last_error)
+// ---------------------------------------------------------------------------
+void set_error(const std::string& msg);
+int fail(int code, const std::string& msg);
+int hip_check(hipError_t e, const char* what);
+
+#define AIMA_REQUIRE(cond, msg)                                   \
+  do {                                                            \
+    if (!(cond)) return ::aima::fail(AIMA_E_INVALID, (msg));      \
+  } while (0)
+
+#define AIMA_HIP(call)                                                  \
+  do {                                                                  \
+    int rc_ = ::aima::hip_check((call), #call);                         \
+    if (rc_ != AIMA_OK) return rc_;                                     \
+  } while (0)
+
+inline bool aligned(const void* p, size_t a) {
+  return (reinterpret_cast<uintptr_t>(p) % a) == 0;
+}
+
+inline bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// Every workspace starts with this header; the error word is the first u32.
+constexpr size_t kWsHeader = 256;
+
+inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Launch status check after a kernel launch.
+int launch_check(const char* what);
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) {
+  return __builtin_bit_cast(f16x2, v);
+}
+__device__ __forceinline__ uint32_t h2_bits(f16x2 v) {
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float h2f(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+// f32 -> f16 round to nearest even (v_cvt_f16_f32 in the default mode).
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ uint32_t u4_code(const uint8_t* packed, int64_t i) {
+  const uint32_t b = packed[i >> 1];
+  return (i & 1) ? (b >> 4) : (b & 0x0fu);
+}
+
+// Wave64 butterfly sum over aligned segments of `width` lanes (power of two);
+// every lane of a segment ends with the segment total.
+template <int WIDTH>
+__device__ __forceinline__ float segment_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// U4 x f16 chunk dot product (32 nibbles of one row against 32 activations).
+//
+// A 32-bit word holds nibbles k0..k7 at bits 0,4,...,28.  Masking with
+// 0x000F000F and OR-ing 0x6400 into each half gives the f16 pair
+// (1024+q0, 1024+q4); masking with 0x00F000F0 gives (1024+16 q1, 1024+16 q5);
+// the same on (word >> 8) gives (q2, q6) and (16 q3, 16 q7).  Two dot2 chains
+// (v_dot2_f32_f16, exact f16 products, f32 accumulate) then hold
+//   a1  = sum_even (1024 + q) x          a16 = sum_odd (1024 + 16 q) x
+// so a1 + a16/16 = sum q x + 1024 X_even + 64 X_odd.  The per-lane constants
+// `bias` = 1024 X_even + 64 X_odd and `xsum` = X_even + X_odd turn that into
+// sum (q - z) x = a1 + a16/16 - bias - z * xsum, exact up to f32 rounding of
+// the running sums (relative error ~1e-5 of the chunk value).
+// ---------------------------------------------------------------------------
+struct XChunk {
+  f16x2 p[16];  // per word d: (x0,x4), (x1,x5), (x2,x6), (x3,x7)
+  float bias;
+  float xsum;
+};
+
+// Build the pairs for 32 consecutive f16 activations given as 16 words.
+__device__ __forceinline__ void make_xchunk(const uint32_t (&xw)[16], XChunk& c) {
+  float xe = 0.f, xo = 0.f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t w0 = xw[4 * d + 0], w1 = xw[4 * d + 1];
+    const uint32_t w2 = xw[4 * d + 2], w3 = xw[4 * d + 3];
+    // words: w0=(x0,x1) w1=(x2,x3) w2=(x4,x5) w3=(x6,x7)
+    c.p[4 * d + 0] = as_h2(__builtin_amdgcn_perm(w2, w0, 0x05040100u));  // (x0,x4)
+    c.p[4 * d + 1] = as_h2(__builtin_amdgcn_perm(w2, w0, 0x07060302u));  // (x1,x5)
+    c.p[4 * d + 2] = as_h2(__builtin_amdgcn_perm(w3, w1, 0x05040100u));  // (x2,x6)
+    c.p[4 * d + 3] = as_h2(__builtin_amdgcn_perm(w3, w1, 0x07060302u));  // (x3,x7)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const f16x2 v = as_h2(xw[4 * d + j]);
+      xe += (float)v.x;
+      xo += (float)v.y;
+    }
+  }
+  c.bias = 1024.f * xe + 64.f * xo;
+  c.xsum = xe + xo;
+}
+
+__device__ __forceinline__ float u4_chunk_raw(const u32x4 w, const XChunk& c) {
+  float a1 = 0.f, a16 = 0.f;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const uint32_t v = w[d];
+    const uint32_t v8 = v >> 8;
+    a1 = __builtin_amdgcn_fdot2(as_h2((v & 0x000F000Fu) | 0x64006400u), c.p[4 * d + 0], a1, false);
+    a16 = __builtin_amdgcn_fdot2(as_h2((v & 0x00F000F0u) | 0x64006400u), c.p[4 * d + 1], a16, false);
+    a1 = __builtin_amdgcn_fdot2(as_h2((v8 & 0x000F000Fu) | 0x64006400u), c.p[4 * d + 2], a1, false);
+    a16 = __builtin_amdgcn_fdot2(as_h2((v8 & 0x00F000F0u) | 0x64006400u), c.p[4 * d + 3], a16, false);
+  }
+  return a1 + a16 * 0.0625f;
+}
+
+// sum_k (q_k - z) * s * x_k over the chunk.
+__device__ __forceinline__ float u4_chunk_dot(const u32x4 w, const XChunk& c,
+                                              uint32_t z, float s) {
+  return (u4_chunk_raw(w, c) - c.bias - (float)z * c.xsum) * s;
+}
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ u32x4 load16_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// Sum over a 256-thread block; every thread gets the total.  `red` is a
+// 4-float shared array.
+__device__ __forceinline__ float block_sum_256(float v, float* red) {
+  v = segment_sum<64>(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+  const float s = g >= 0.f ? 1.f / (1.f + expf(-g)) : expf(g) / (1.f + expf(g));
+  return g * s * u;
+}
+
+}  // namespace aima

@@ -1,0 +1,482 @@
+// Batch-1 MoE FFN decode on gfx950: two bandwidth-bound launches per layer.
+//
+// Phase A (gate/up + SwiGLU): the k routed experts and the shared expert form
+// (k+1)*I row pairs (gate row j, up row I+j).  Each wave streams two pairs
+// (4 rows of H/2 bytes) with 128-bit loads, reduces each row across its lane
+// segment and applies silu(gate)*up in registers; the activation is stored as
+// f16 [k+1][I].  Block 0 also evaluates the shared expert's scalar gate
+// sigmoid(gate_vec . h).
+//
+// Phase B (down + aggregate + residual): each block owns 8 output rows.  Its
+// four waves split the k+1 down matrices (slot s -> wave s % 4), each lane
+// accumulates w_s * (row . act_s) over its slots, and the four partial sums
+// plus the residual are added in a fixed order: no atomics, deterministic.
+#include "common.h"
+
+#include <math.h>
+
+namespace aima {
+
+constexpr int kPairsPerWave = 2;
+constexpr int kDownRowsPerBlock = 8;
+
+struct DecodeWs {
+  uint32_t* err;
+  uint16_t* act;   // [(k+1)][I] f16
+  float* sigma;    // shared-expert gate
+  uint16_t* h;     // [H] normalized input (stack only)
+  uint16_t* r[2];  // [H] residual ping-pong (stack only)
+};
+
+static size_t decode_ws_bytes(int64_t hidden, int64_t inter, int k, bool stack) {
+  size_t b = kWsHeader;
+  b += round_up((size_t)(k + 1) * inter * 2, 256);
+  b += 256;
+  if (stack) b += 3 * round_up((size_t)hidden * 2, 256);
+  return b;
+}
+
+static DecodeWs decode_ws(void* ws, int64_t hidden, int64_t inter, int k, bool stack) {
+  DecodeWs w{};
+  char* p = static_cast<char*>(ws);
+  w.err = reinterpret_cast<uint32_t*>(p);
+  p += kWsHeader;
+  w.act = reinterpret_cast<uint16_t*>(p);
+  p += round_up((size_t)(k + 1) * inter * 2, 256);
+  w.sigma = reinterpret_cast<float*>(p);
+  p += 256;
+  if (stack) {
+    w.h = reinterpret_cast<uint16_t*>(p);
+    p += round_up((size_t)hidden * 2, 256);
+    w.r[0] = reinterpret_cast<uint16_t*>(p);
+    p += round_up((size_t)hidden * 2, 256);
+    w.r[1] = reinterpret_cast<uint16_t*>(p);
+  }
+  return w;
+}
+
+template <int KCH>
+struct Geom {
+  static constexpr int NC = KCH > 64 ? KCH / 64 : 1;
+  static constexpr int SEG = KCH > 64 ? 64 : KCH;
+  static constexpr int RPI = 64 / SEG;
+  static constexpr int K = KCH * 32;
+};
+
+template <int KCH>
+__device__ __forceinline__ void load_chunks(const uint16_t* __restrict__ x, int cl,
+                                            XChunk (&xc)[Geom<KCH>::NC]) {
+  using G = Geom<KCH>;
+#pragma unroll
+  for (int i = 0; i < G::NC; ++i) {
+    const int c = cl + i * G::SEG;
+    const u32x4* p = reinterpret_cast<const u32x4*>(x + (int64_t)c * 32);
+    uint32_t w[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 v = p[q];
+      w[4 * q + 0] = v[0];
+      w[4 * q + 1] = v[1];
+      w[4 * q + 2] = v[2];
+      w[4 * q + 3] = v[3];
+    }
+    make_xchunk(w, xc[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// phase A
+// ---------------------------------------------------------------------------
+template <int KCH>
+__global__ __launch_bounds__(256) void decode_gateup_kernel(
+    const uint16_t* __restrict__ x, aima_moe_layer L, const int32_t* __restrict__ ids,
+    int k, uint32_t* __restrict__ err, uint16_t* __restrict__ act,
+    float* __restrict__ sigma) {
+  using G = Geom<KCH>;
+  constexpr int NR = 2 * kPairsPerWave;          // rows per wave
+  constexpr int PASSES = (NR + G::RPI - 1) / G::RPI;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int seg = lane / G::SEG;
+  const int cl = lane % G::SEG;
+  const int64_t I = L.inter;
+  const int64_t groups = G::K / L.group;
+  const int64_t total_pairs = (int64_t)(k + 1) * I;
+  const int64_t pair0 = ((int64_t)blockIdx.x * 4 + wave) * kPairsPerWave;
+
+  XChunk xc[G::NC];
+  load_chunks<KCH>(x, cl, xc);
+
+  u32x4 w[PASSES][G::NC];
+  float s[PASSES][G::NC];
+  uint32_t z[PASSES][G::NC];
+  bool ok[PASSES];
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int ri = ps * G::RPI + seg;  // row index in this wave's list
+    const int64_t pair = pair0 + ri / 2;
+    const bool up = ri & 1;
+    bool valid = ri < NR && pair < total_pairs;
+    const uint8_t* qw = nullptr;
+    const uint16_t* sc = nullptr;
+    const uint8_t* zp = nullptr;
+    int64_t row = 0;
+    if (valid) {
+      const int64_t slot = pair / I;
+      const int64_t j = pair - slot * I;
+      row = (up ? I : 0) + j;
+      const int64_t rows_e = 2 * I;
+      if (slot < k) {
+        const int32_t e = ids[slot];
+        if (e < 0 || e >= L.experts) {
+          if (j == 0 && !up && cl == 0) atomicOr(err, AIMA_DEVERR_EXPERT_RANGE);
+          valid = false;
+        } else {
+          qw = L.gate_up.qweight + (int64_t)e * rows_e * (G::K / 2);
+          sc = L.gate_up.scale + (int64_t)e * rows_e * groups;
+          zp = L.gate_up.zp + (int64_t)e * (rows_e * groups / 2);
+        }
+      } else {
+        qw = L.shared_gate_up.qweight;
+        sc = L.shared_gate_up.scale;
+        zp = L.shared_gate_up.zp;
+      }
+    }
+    ok[ps] = valid;
+#pragma unroll
+    for (int i = 0; i < G::NC; ++i) {
+      const int c = cl + i * G::SEG;
+      if (valid) {
+        w[ps][i] = load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16);
+        const int64_t gi = row * groups + ((int64_t)c * 32) / L.group;
+        s[ps][i] = h2f(sc[gi]);
+        z[ps][i] = u4_code(zp, gi);
+      } else {
+        w[ps][i] = u32x4{0u, 0u, 0u, 0u};
+        s[ps][i] = 0.f;
+        z[ps][i] = 0u;
+      }
+    }
+  }
+  float v[PASSES];
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < G::NC; ++i) acc += u4_chunk_dot(w[ps][i], xc[i], z[ps][i], s[ps][i]);
+    v[ps] = ok[ps] ? segment_sum<G::SEG>(acc) : 0.f;
+  }
+  // Gather the NR row sums: row ri lives in segment (ri % RPI) of pass ri / RPI.
+  float rows[NR];
+#pragma unroll
+  for (int ri = 0; ri < NR; ++ri) rows[ri] = __shfl(v[ri / G::RPI], (ri % G::RPI) * G::SEG, 64);
+  if (lane < kPairsPerWave) {
+    const int64_t pair = pair0 + lane;
+    if (pair < total_pairs) {
+      float g = 0.f, u = 0.f;
+#pragma unroll
+      for (int p = 0; p < kPairsPerWave; ++p) {
+        if (p == lane) {
+          g = rows[2 * p];
+          u = rows[2 * p + 1];
+        }
+      }
+      act[pair] = f2h(silu_mul(g, u));
+    }
+  }
+  if (blockIdx.x == 0 && wave == 0) {
+    float acc = 0.f;
+    for (int64_t i = lane; i < L.hidden; i += 64) acc += h2f(L.shared_gate_vec[i]) * h2f(x[i]);
+    acc = segment_sum<64>(acc);
+    if (lane == 0) {
+      const double t = acc;
+      const double r = t >= 0.0 ? 1.0 / (1.0 + exp(-t)) : exp(t) / (1.0 + exp(t));
+      *sigma = (float)r;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// phase B
+// ---------------------------------------------------------------------------
+template <int KCH>
+__global__ __launch_bounds__(256) void decode_down_kernel(
+    aima_moe_layer L, const int32_t* __restrict__ ids, const float* __restrict__ rw, int k,
+    const uint16_t* __restrict__ act, const float* __restrict__ sigma,
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out) {
+  using G = Geom<KCH>;
+  constexpr int PASSES = (kDownRowsPerBlock + G::RPI - 1) / G::RPI;
+  __shared__ float part[4][PASSES * G::RPI];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int seg = lane / G::SEG;
+  const int cl = lane % G::SEG;
+  const int64_t H = L.hidden;
+  const int64_t I = L.inter;
+  const int64_t groups = G::K / L.group;
+  const int64_t h0 = (int64_t)blockIdx.x * kDownRowsPerBlock;
+
+  float acc[PASSES];
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) acc[ps] = 0.f;
+
+  for (int slot = wave; slot <= k; slot += 4) {
+    const uint8_t* qw;
+    const uint16_t* sc;
+    const uint8_t* zp;
+    float coef;
+    if (slot < k) {
+      const int32_t e = ids[slot];
+      if (e < 0 || e >= L.experts) continue;  // flagged by phase A
+      qw = L.down.qweight + (int64_t)e * H * (G::K / 2);
+      sc = L.down.scale + (int64_t)e * H * groups;
+      zp = L.down.zp + (int64_t)e * (H * groups / 2);
+      coef = rw[slot];
+    } else {
+      qw = L.shared_down.qweight;
+      sc = L.shared_down.scale;
+      zp = L.shared_down.zp;
+      coef = *sigma;
+    }
+    u32x4 w[PASSES][G::NC];
+    float s[PASSES][G::NC];
+    uint32_t z[PASSES][G::NC];
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      const int64_t row = h0 + ps * G::RPI + seg;
+#pragma unroll
+      for (int i = 0; i < G::NC; ++i) {
+        const int c = cl + i * G::SEG;
+        if (ps * G::RPI + seg < kDownRowsPerBlock && row < H) {
+          w[ps][i] = load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16);
+          const int64_t gi = row * groups + ((int64_t)c * 32) / L.group;
+          s[ps][i] = h2f(sc[gi]);
+          z[ps][i] = u4_code(zp, gi);
+        } else {
+          w[ps][i] = u32x4{0u, 0u, 0u, 0u};
+          s[ps][i] = 0.f;
+          z[ps][i] = 0u;
+        }
+      }
+    }
+    XChunk xc[G::NC];
+    load_chunks<KCH>(act + (int64_t)slot * I, cl, xc);
+#pragma unroll
+    for (int ps = 0; ps < PASSES; ++ps) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < G::NC; ++i) d += u4_chunk_dot(w[ps][i], xc[i], z[ps][i], s[ps][i]);
+      acc[ps] += coef * d;
+    }
+  }
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const float t = segment_sum<G::SEG>(acc[ps]);
+    if (cl == 0) part[wave][ps * G::RPI + seg] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < kDownRowsPerBlock) {
+    const int64_t row = h0 + threadIdx.x;
+    if (row < H) {
+      const float f = ((part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x]) +
+                      part[3][threadIdx.x];
+      const float r = residual ? h2f(residual[row]) : 0.f;
+      out[row] = f2h(r + f);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+static int check_layer(const aima_moe_layer* L, int k, bool need_norm) {
+  AIMA_REQUIRE(L != nullptr, "moe: null layer");
+  AIMA_REQUIRE(L->gate_up.qweight && L->gate_up.scale && L->gate_up.zp,
+               "moe: null routed gate/up tensor");
+  AIMA_REQUIRE(L->down.qweight && L->down.scale && L->down.zp, "moe: null routed down tensor");
+  AIMA_REQUIRE(L->shared_gate_up.qweight && L->shared_gate_up.scale && L->shared_gate_up.zp,
+               "moe: null shared gate/up tensor");
+  AIMA_REQUIRE(L->shared_down.qweight && L->shared_down.scale && L->shared_down.zp,
+               "moe: null shared down tensor");
+  AIMA_REQUIRE(L->shared_gate_vec != nullptr, "moe: null shared gate vector");
+  AIMA_REQUIRE(!need_norm || L->norm_weight != nullptr, "moe: null norm weight");
+  AIMA_REQUIRE(L->experts > 0 && k > 0 && k <= L->experts, "moe: need 0 < k <= experts");
+  AIMA_REQUIRE(L->shared_inter == L->inter, "moe: shared_inter must equal inter");
+  AIMA_REQUIRE(L->group == 32 || L->group == 64 || L->group == 128 || L->group == 256,
+               "moe: group must be 32, 64, 128 or 256");
+  AIMA_REQUIRE(L->hidden % L->group == 0 && L->inter % L->group == 0,
+               "moe: hidden and inter must be multiples of group");
+  AIMA_REQUIRE(aligned(L->gate_up.qweight, 16) && aligned(L->down.qweight, 16) &&
+                   aligned(L->shared_gate_up.qweight, 16) && aligned(L->shared_down.qweight, 16),
+               "moe: qweight pointers must be 16-byte aligned");
+  return AIMA_OK;
+}
+
+static bool decode_shape_ok(const aima_moe_layer* L) {
+  const int64_t hk = L->hidden / 32, ik = L->inter / 32;
+  return L->hidden % 32 == 0 && L->inter % 32 == 0 && (hk == 16 || hk == 32 || hk == 64 ||
+         hk == 128) && (ik == 4 || ik == 8 || ik == 16 || ik == 32 || ik == 64);
+}
+
+template <int KCH>
+static void launch_gateup(const uint16_t* x, const aima_moe_layer& L, const int32_t* ids, int k,
+                          const DecodeWs& w, hipStream_t st) {
+  const int64_t pairs = (int64_t)(k + 1) * L.inter;
+  const int64_t waves = (pairs + kPairsPerWave - 1) / kPairsPerWave;
+  const int64_t blocks = (waves + 3) / 4;
+  hipLaunchKernelGGL((decode_gateup_kernel<KCH>), dim3((unsigned)blocks), dim3(256), 0, st, x, L,
+                     ids, k, w.err, w.act, w.sigma);
+}
+
+template <int KCH>
+static void launch_down(const aima_moe_layer& L, const int32_t* ids, const float* rw, int k,
+                        const DecodeWs& w, const uint16_t* residual, uint16_t* out,
+                        hipStream_t st) {
+  const int64_t blocks = (L.hidden + kDownRowsPerBlock - 1) / kDownRowsPerBlock;
+  hipLaunchKernelGGL((decode_down_kernel<KCH>), dim3((unsigned)blocks), dim3(256), 0, st, L, ids,
+                     rw, k, w.act, w.sigma, residual, out);
+}
+
+static int decode_layer(const aima_moe_layer& L, const uint16_t* x, const uint16_t* residual,
+                        const int32_t* ids, const float* rw, int k, uint16_t* out,
+                        const DecodeWs& w, hipStream_t st) {
+  switch (L.hidden / 32) {
+    case 16: launch_gateup<16>(x, L, ids, k, w, st); break;
+    case 32: launch_gateup<32>(x, L, ids, k, w, st); break;
+    case 64: launch_gateup<64>(x, L, ids, k, w, st); break;
+    case 128: launch_gateup<128>(x, L, ids, k, w, st); break;
+    default: return fail(AIMA_E_UNSUPPORTED, "moe decode: unsupported hidden size");
+  }
+  int rc = launch_check("moe decode gate/up");
+  if (rc != AIMA_OK) return rc;
+  switch (L.inter / 32) {
+    case 4: launch_down<4>(L, ids, rw, k, w, residual, out, st); break;
+    case 8: launch_down<8>(L, ids, rw, k, w, residual, out, st); break;
+    case 16: launch_down<16>(L, ids, rw, k, w, residual, out, st); break;
+    case 32: launch_down<32>(L, ids, rw, k, w, residual, out, st); break;
+    case 64: launch_down<64>(L, ids, rw, k, w, residual, out, st); break;
+    default: return fail(AIMA_E_UNSUPPORTED, "moe decode: unsupported intermediate size");
+  }
+  return launch_check("moe decode down");
+}
+
+int rmsnorm_launch(const uint16_t* x, const float* weight, int64_t rows, int64_t hidden,
+                   float eps, uint16_t* out, hipStream_t st);
+
+}  // namespace aima
+
+using namespace aima;
+
+extern "C" int aima_moe_decode_workspace_size(const aima_moe_layer* layer, int32_t k,
+                                              size_t* bytes) {
+  AIMA_REQUIRE(layer && bytes, "moe_decode_workspace_size: null pointer");
+  AIMA_REQUIRE(k > 0, "moe_decode_workspace_size: k must be positive");
+  *bytes = decode_ws_bytes(layer->hidden, layer->inter, k, true);
+  return AIMA_OK;
+}
+
+extern "C" int aima_moe_ffn_decode(const aima_moe_layer* layer, const uint16_t* x,
+                                   const uint16_t* residual, const int32_t* ids,
+                                   const float* weights, int32_t k, uint16_t* out,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_layer(layer, k, false);
+  if (rc != AIMA_OK) return rc;
+  AIMA_REQUIRE(x && ids && weights && out, "moe_ffn_decode: null pointer");
+  AIMA_REQUIRE(aligned(x, 16), "moe_ffn_decode: x must be 16-byte aligned");
+  if (!decode_shape_ok(layer)) {
+    return fail(AIMA_E_UNSUPPORTED, "moe_ffn_decode: hidden/32 must be 16..128 and inter/32 4..64 (powers of two)");
+  }
+  if (!workspace || workspace_bytes < decode_ws_bytes(layer->hidden, layer->inter, k, false)) {
+    return fail(AIMA_E_WORKSPACE, "moe_ffn_decode: workspace missing or too small");
+  }
+  AIMA_REQUIRE(aligned(workspace, 256), "moe_ffn_decode: workspace must be 256-byte aligned");
+  const DecodeWs w = decode_ws(workspace, layer->hidden, layer->inter, k, false);
+  return decode_layer(*layer, x, residual, ids, weights, k, out, w, (hipStream_t)stream);
+}
+
+extern "C" int aima_moe_decode_gate_up(const aima_moe_layer* layer, const uint16_t* x,
+                                       const int32_t* ids, int32_t k, uint16_t* act,
+                                       float* shared_sigma, uint32_t* error_word,
+                                       void* stream) {
+  int rc = check_layer(layer, k, false);
+  if (rc != AIMA_OK) return rc;
+  AIMA_REQUIRE(x && ids && act && shared_sigma && error_word, "moe_decode_gate_up: null pointer");
+  AIMA_REQUIRE(aligned(x, 16), "moe_decode_gate_up: x must be 16-byte aligned");
+  if (!decode_shape_ok(layer)) {
+    return fail(AIMA_E_UNSUPPORTED, "moe_decode_gate_up: unsupported hidden/inter");
+  }
+  DecodeWs w{};
+  w.err = error_word;
+  w.act = act;
+  w.sigma = shared_sigma;
+  hipStream_t st = (hipStream_t)stream;
+  switch (layer->hidden / 32) {
+    case 16: launch_gateup<16>(x, *layer, ids, k, w, st); break;
+    case 32: launch_gateup<32>(x, *layer, ids, k, w, st); break;
+    case 64: launch_gateup<64>(x, *layer, ids, k, w, st); break;
+    case 128: launch_gateup<128>(x, *layer, ids, k, w, st); break;
+    default: return fail(AIMA_E_UNSUPPORTED, "moe decode: unsupported hidden size");
+  }
+  return launch_check("moe decode gate/up");
+}
+
+extern "C" int aima_moe_decode_down(const aima_moe_layer* layer, const uint16_t* act,
+                                    const float* shared_sigma, const int32_t* ids,
+                                    const float* weights, int32_t k, const uint16_t* residual,
+                                    uint16_t* out, void* stream) {
+  int rc = check_layer(layer, k, false);
+  if (rc != AIMA_OK) return rc;
+  AIMA_REQUIRE(act && shared_sigma && ids && weights && out, "moe_decode_down: null pointer");
+  AIMA_REQUIRE(aligned(act, 16), "moe_decode_down: act must be 16-byte aligned");
+  if (!decode_shape_ok(layer)) {
+    return fail(AIMA_E_UNSUPPORTED, "moe_decode_down: unsupported hidden/inter");
+  }
+  DecodeWs w{};
+  w.act = const_cast<uint16_t*>(act);
+  w.sigma = const_cast<float*>(shared_sigma);
+  hipStream_t st = (hipStream_t)stream;
+  switch (layer->inter / 32) {
+    case 4: launch_down<4>(*layer, ids, weights, k, w, residual, out, st); break;
+    case 8: launch_down<8>(*layer, ids, weights, k, w, residual, out, st); break;
+    case 16: launch_down<16>(*layer, ids, weights, k, w, residual, out, st); break;
+    case 32: launch_down<32>(*layer, ids, weights, k, w, residual, out, st); break;
+    case 64: launch_down<64>(*layer, ids, weights, k, w, residual, out, st); break;
+    default: return fail(AIMA_E_UNSUPPORTED, "moe decode: unsupported intermediate size");
+  }
+  return launch_check("moe decode down");
+}
+
+extern "C" int aima_moe_stack_decode(const aima_moe_layer* layers, int32_t n_layers, float eps,
+                                     const uint16_t* residual_in, const int32_t* ids,
+                                     const float* weights, int32_t k, uint16_t* out,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  AIMA_REQUIRE(layers && n_layers > 0, "moe_stack_decode: need at least one layer");
+  AIMA_REQUIRE(residual_in && ids && weights && out, "moe_stack_decode: null pointer");
+  for (int32_t l = 0; l < n_layers; ++l) {
+    int rc = check_layer(&layers[l], k, true);
+    if (rc != AIMA_OK) return rc;
+    AIMA_REQUIRE(layers[l].hidden == layers[0].hidden && layers[l].inter == layers[0].inter,
+                 "moe_stack_decode: all layers must share hidden and inter");
+  }
+  if (!decode_shape_ok(&layers[0])) {
+    return fail(AIMA_E_UNSUPPORTED, "moe_stack_decode: unsupported hidden/inter");
+  }
+  const size_t need = decode_ws_bytes(layers[0].hidden, layers[0].inter, k, true);
+  if (!workspace || workspace_bytes < need) {
+    return fail(AIMA_E_WORKSPACE, "moe_stack_decode: workspace missing or too small");
+  }
+  AIMA_REQUIRE(aligned(workspace, 256), "moe_stack_decode: workspace must be 256-byte aligned");
+  const DecodeWs w = decode_ws(workspace, layers[0].hidden, layers[0].inter, k, true);
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* r = residual_in;
+  for (int32_t l = 0; l < n_layers; ++l) {
+    const aima_moe_layer& L = layers[l];
+    int rc = rmsnorm_launch(r, L.norm_weight, 1, L.hidden, eps, w.h, st);
+    if (rc != AIMA_OK) return rc;
+    uint16_t* dst = (l == n_layers - 1) ? out : w.r[l & 1];
+    rc = decode_layer(L, w.h, r, ids + (int64_t)l * k, weights + (int64_t)l * k, k, dst, w, st);
+    if (rc != AIMA_OK) return rc;
+    r = dst;
+  }
+  return AIMA_OK;
+}

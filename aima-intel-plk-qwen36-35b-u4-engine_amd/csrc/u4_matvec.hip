@@ -1,0 +1,334 @@
+// U4 dequant, batch-1 U4 matvec, RMSNorm and router top-k for gfx950.
+//
+// Decode matvec: each row of K/2 packed bytes is split into 16-byte chunks
+// (32 nibbles, always inside one quantization group because group % 32 == 0).
+// A wave covers 64 chunks: one row at K=2048, four rows at K=512.  Every lane
+// issues one 128-bit global load per row, unpacks in registers and reduces
+// with two v_dot2_f32_f16 chains (see XChunk in common.h), then the row's
+// segment is reduced across lanes.  Row groups are loaded before any compute
+// so each wave keeps RG x 1 KB in flight.
+#include "common.h"
+
+#include <math.h>
+
+namespace aima {
+
+// ---------------------------------------------------------------------------
+// dequant: out[n][k] = f32(q - z) * f32(s), one thread per 8 codes
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void u4_dequant_kernel(
+    const uint32_t* __restrict__ qw, const uint16_t* __restrict__ scale,
+    const uint8_t* __restrict__ zp, int64_t words, int64_t k, int group,
+    float4* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= words) return;
+  const int64_t words_per_row = k / 8;
+  const int64_t row = i / words_per_row;
+  const int64_t k0 = (i % words_per_row) * 8;
+  const int64_t groups = k / group;
+  const int64_t gi = row * groups + k0 / group;
+  const float s = h2f(scale[gi]);
+  const int z = (int)u4_code(zp, gi);
+  const uint32_t v = qw[i];
+  float f[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) f[j] = (float)((int)((v >> (4 * j)) & 0xfu) - z) * s;
+  out[2 * i] = make_float4(f[0], f[1], f[2], f[3]);
+  out[2 * i + 1] = make_float4(f[4], f[5], f[6], f[7]);
+}
+
+// ---------------------------------------------------------------------------
+// matvec
+// ---------------------------------------------------------------------------
+template <int KCH>
+struct RowGeom {
+  static constexpr int NC = KCH > 64 ? KCH / 64 : 1;  // chunks per lane per row
+  static constexpr int SEG = KCH > 64 ? 64 : KCH;     // lanes per row
+  static constexpr int RPI = 64 / SEG;                // rows per wave pass
+  static constexpr int K = KCH * 32;
+};
+
+// Load the lane's activation chunks (chunk c = cl + i*SEG) from f16 x.
+template <int KCH>
+__device__ __forceinline__ void load_x_chunks(const uint16_t* __restrict__ x,
+                                              int cl, XChunk (&xc)[RowGeom<KCH>::NC]) {
+  using G = RowGeom<KCH>;
+#pragma unroll
+  for (int i = 0; i < G::NC; ++i) {
+    const int c = cl + i * G::SEG;
+    const u32x4* p = reinterpret_cast<const u32x4*>(x + (int64_t)c * 32);
+    uint32_t w[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 v = p[q];
+      w[4 * q + 0] = v[0];
+      w[4 * q + 1] = v[1];
+      w[4 * q + 2] = v[2];
+      w[4 * q + 3] = v[3];
+    }
+    make_xchunk(w, xc[i]);
+  }
+}
+
+template <int KCH, int RG>
+__global__ __launch_bounds__(256) void u4_matvec_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ qw,
+    const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zp,
+    int64_t n, int group_log2, void* __restrict__ y, int out_f32) {
+  using G = RowGeom<KCH>;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int seg = lane / G::SEG;
+  const int cl = lane % G::SEG;
+  const int64_t groups = (int64_t)G::K >> group_log2;
+
+  XChunk xc[G::NC];
+  load_x_chunks<KCH>(x, cl, xc);
+
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * (RG * G::RPI);
+  u32x4 w[RG][G::NC];
+  float s[RG][G::NC];
+  uint32_t z[RG][G::NC];
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int64_t row = row0 + r * G::RPI + seg;
+#pragma unroll
+    for (int i = 0; i < G::NC; ++i) {
+      const int c = cl + i * G::SEG;
+      if (row < n) {
+        w[r][i] = load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16);
+        const int64_t gi = row * groups + (((int64_t)c * 32) >> group_log2);
+        s[r][i] = h2f(scale[gi]);
+        z[r][i] = u4_code(zp, gi);
+      } else {
+        w[r][i] = u32x4{0u, 0u, 0u, 0u};
+        s[r][i] = 0.f;
+        z[r][i] = 0u;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int64_t row = row0 + r * G::RPI + seg;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < G::NC; ++i) acc += u4_chunk_dot(w[r][i], xc[i], z[r][i], s[r][i]);
+    acc = segment_sum<G::SEG>(acc);
+    if (cl == 0 && row < n) {
+      if (out_f32) {
+        reinterpret_cast<float*>(y)[row] = acc;
+      } else {
+        reinterpret_cast<uint16_t*>(y)[row] = f2h(acc);
+      }
+    }
+  }
+}
+
+template <int KCH>
+static void launch_matvec(const uint16_t* x, const uint8_t* qw, const uint16_t* scale,
+                          const uint8_t* zp, int64_t n, int glog2, void* y, int out_f32,
+                          hipStream_t st) {
+  constexpr int RG = 4;
+  const int64_t rows_per_block = 4 * RG * RowGeom<KCH>::RPI;
+  const int64_t blocks = (n + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((u4_matvec_kernel<KCH, RG>), dim3((unsigned)blocks), dim3(256), 0, st,
+                     x, qw, scale, zp, n, glog2, y, out_f32);
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm: one 256-thread block per row
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                      const float* __restrict__ weight,
+                                                      int64_t hidden, float eps,
+                                                      uint16_t* __restrict__ out) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * hidden;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < hidden; i += 256) {
+    const float v = h2f(xr[i]);
+    ss += v * v;
+  }
+  ss = block_sum_256(ss, red);
+  const float scale = 1.0f / sqrtf(ss / (float)hidden + eps);
+  for (int64_t i = threadIdx.x; i < hidden; i += 256) {
+    out[row * hidden + i] = f2h(h2f(xr[i]) * scale * weight[i]);
+  }
+}
+
+int rmsnorm_launch(const uint16_t* x, const float* weight, int64_t rows, int64_t hidden,
+                   float eps, uint16_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, weight, hidden,
+                     eps, out);
+  return launch_check("rmsnorm");
+}
+
+// ---------------------------------------------------------------------------
+// Router top-k: one wave per token.  f64 softmax (gguf_loader.cpp:3646-3670),
+// selection by (probability desc, id asc) (gguf_loader.cpp:3672-3697),
+// renormalization by max(sum, min) in f32 (gguf_loader.cpp:3712-3731).
+// ---------------------------------------------------------------------------
+constexpr int kRouterMaxPerLane = 16;  // experts <= 1024
+
+__global__ __launch_bounds__(256) void router_topk_kernel(
+    const float* __restrict__ logits, int64_t tokens, int experts, int k,
+    float min_weight_sum, int32_t* __restrict__ ids, float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int64_t token = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (token >= tokens) return;
+  const float* l = logits + token * experts;
+  const int per = (experts + 63) / 64;
+  float v[kRouterMaxPerLane];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kRouterMaxPerLane; ++j) {
+    const int i = lane + 64 * j;
+    v[j] = (j < per && i < experts) ? l[i] : -INFINITY;
+    mx = fmaxf(mx, v[j]);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  double e[kRouterMaxPerLane];
+  double sum = 0.0;
+#pragma unroll
+  for (int j = 0; j < kRouterMaxPerLane; ++j) {
+    const int i = lane + 64 * j;
+    e[j] = (j < per && i < experts) ? exp((double)v[j] - (double)mx) : 0.0;
+    sum += e[j];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  float p[kRouterMaxPerLane];
+#pragma unroll
+  for (int j = 0; j < kRouterMaxPerLane; ++j) {
+    const int i = lane + 64 * j;
+    p[j] = (j < per && i < experts) ? (float)(e[j] / sum) : -INFINITY;
+  }
+  float sel_p[16];
+  int sel_i[16];
+  for (int r = 0; r < k; ++r) {
+    float bp = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < kRouterMaxPerLane; ++j) {
+      const int i = lane + 64 * j;
+      if (i < experts && (p[j] > bp || (p[j] == bp && i < bi))) {
+        bp = p[j];
+        bi = i;
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      const float op = __shfl_xor(bp, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (op > bp || (op == bp && oi < bi)) {
+        bp = op;
+        bi = oi;
+      }
+    }
+    sel_p[r] = bp;
+    sel_i[r] = bi;
+#pragma unroll
+    for (int j = 0; j < kRouterMaxPerLane; ++j) {
+      if (lane + 64 * j == bi) p[j] = -INFINITY;
+    }
+  }
+  if (lane == 0) {
+    float s = 0.f;
+    for (int r = 0; r < k; ++r) s += sel_p[r];
+    const float den = s > min_weight_sum ? s : min_weight_sum;
+    for (int r = 0; r < k; ++r) {
+      ids[token * k + r] = sel_i[r];
+      weights[token * k + r] = sel_p[r] / den;
+    }
+  }
+}
+
+int u4_matvec_dispatch(const uint16_t* x, const uint8_t* qw, const uint16_t* scale,
+                       const uint8_t* zp, int64_t n, int64_t k, int glog2, void* y,
+                       int out_f32, hipStream_t st) {
+  switch (k) {
+    case 128: launch_matvec<4>(x, qw, scale, zp, n, glog2, y, out_f32, st); break;
+    case 256: launch_matvec<8>(x, qw, scale, zp, n, glog2, y, out_f32, st); break;
+    case 512: launch_matvec<16>(x, qw, scale, zp, n, glog2, y, out_f32, st); break;
+    case 1024: launch_matvec<32>(x, qw, scale, zp, n, glog2, y, out_f32, st); break;
+    case 2048: launch_matvec<64>(x, qw, scale, zp, n, glog2, y, out_f32, st); break;
+    case 4096: launch_matvec<128>(x, qw, scale, zp, n, glog2, y, out_f32, st); break;
+    case 8192: launch_matvec<256>(x, qw, scale, zp, n, glog2, y, out_f32, st); break;
+    default:
+      return fail(AIMA_E_UNSUPPORTED, "u4_matvec: K must be a power of two in [128, 8192]");
+  }
+  return launch_check("u4_matvec");
+}
+
+int group_log2_of(int group) {
+  switch (group) {
+    case 32: return 5;
+    case 64: return 6;
+    case 128: return 7;
+    case 256: return 8;
+    default: return -1;
+  }
+}
+
+}  // namespace aima
+
+using namespace aima;
+
+extern "C" int aima_u4_dequant(const uint8_t* qweight, const uint16_t* scale,
+                               const uint8_t* zp, int64_t n, int64_t k, int32_t group,
+                               float* out, void* stream) {
+  AIMA_REQUIRE(qweight && scale && zp && out, "u4_dequant: null pointer");
+  AIMA_REQUIRE(n > 0 && k > 0, "u4_dequant: n and k must be positive");
+  AIMA_REQUIRE(group > 0 && group % 32 == 0 && k % group == 0,
+               "u4_dequant: group must be a multiple of 32 dividing k");
+  AIMA_REQUIRE(aligned(qweight, 4) && aligned(out, 16), "u4_dequant: misaligned pointer");
+  const int64_t words = n * k / 8;
+  const int64_t blocks = (words + 255) / 256;
+  hipLaunchKernelGGL(u4_dequant_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const uint32_t*>(qweight),
+                     scale, zp, words, k, (int)group, reinterpret_cast<float4*>(out));
+  return launch_check("u4_dequant");
+}
+
+extern "C" int aima_u4_matvec(const uint16_t* x, const uint8_t* qweight,
+                              const uint16_t* scale, const uint8_t* zp, int64_t n,
+                              int64_t k, int32_t group, void* y, int32_t out_dtype,
+                              void* stream) {
+  AIMA_REQUIRE(x && qweight && scale && zp && y, "u4_matvec: null pointer");
+  AIMA_REQUIRE(n > 0, "u4_matvec: n must be positive");
+  AIMA_REQUIRE(out_dtype == AIMA_OUT_F16 || out_dtype == AIMA_OUT_F32,
+               "u4_matvec: out_dtype must be AIMA_OUT_F16 or AIMA_OUT_F32");
+  const int glog2 = group_log2_of(group);
+  AIMA_REQUIRE(glog2 > 0, "u4_matvec: group must be 32, 64, 128 or 256");
+  AIMA_REQUIRE(k % group == 0, "u4_matvec: k must be a multiple of group");
+  AIMA_REQUIRE(aligned(qweight, 16) && aligned(x, 16),
+               "u4_matvec: qweight and x must be 16-byte aligned");
+  return u4_matvec_dispatch(x, qweight, scale, zp, n, k, glog2, y, out_dtype,
+                            (hipStream_t)stream);
+}
+
+extern "C" int aima_rmsnorm(const uint16_t* x, const float* weight, int64_t rows,
+                            int64_t hidden, float eps, uint16_t* out, void* stream) {
+  AIMA_REQUIRE(x && weight && out, "rmsnorm: null pointer");
+  AIMA_REQUIRE(rows > 0 && hidden > 0, "rmsnorm: rows and hidden must be positive");
+  AIMA_REQUIRE(rows <= 0x7fffffff, "rmsnorm: too many rows");
+  return rmsnorm_launch(x, weight, rows, hidden, eps, out, (hipStream_t)stream);
+}
+
+extern "C" int aima_router_topk(const float* logits, int64_t tokens, int32_t experts,
+                                int32_t k, float min_weight_sum, int32_t* ids,
+                                float* weights, void* stream) {
+  AIMA_REQUIRE(logits && ids && weights, "router_topk: null pointer");
+  AIMA_REQUIRE(tokens > 0, "router_topk: tokens must be positive");
+  AIMA_REQUIRE(experts > 0 && experts <= 64 * kRouterMaxPerLane,
+               "router_topk: experts must be in [1, 1024]");
+  AIMA_REQUIRE(k > 0 && k <= 16 && k <= experts, "router_topk: k must be in [1, min(16, experts)]");
+  AIMA_REQUIRE(min_weight_sum > 0.f, "router_topk: minimum weight sum must be positive");
+  const int64_t blocks = (tokens + 3) / 4;
+  hipLaunchKernelGGL(router_topk_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     (hipStream_t)stream, logits, tokens, experts, k, min_weight_sum, ids,
+                     weights);
+  return launch_check("router_topk");
+}

@@ -1,0 +1,322 @@
+"""Host API of the U4 MoE hot path (PyTorch tensors in, PyTorch tensors out).
+
+Each function validates shapes on the host, then calls one C-ABI entry point
+on torch's current HIP stream.  Names mirror the reference interfaces they
+replace:
+
+* ``matvec_u4``            <- ``iq36_fixed_fc1`` / ``matvec_tensor``
+* ``apply_rms_norm``       <- ``apply_rms_norm`` (gguf_loader.hpp:355-357)
+* ``select_router_topk``   <- ``select_router_topk`` (gguf_loader.hpp:371-373)
+* ``run_moe_ffn_layer``    <- ``run_qwen36_moe_ffn_layer``'s expert part
+  (gguf_loader.hpp:519-524, gguf_loader.cpp:5711-5780)
+* ``grouped_moe_prefill``  <- ``GroupedS8U4PrefillRuntime::RunLayer`` /
+  ``MOE3GemmFusedCompressed``
+* ``build_grouped_schedule`` <- ``BuildGroupedSchedule``
+  (grouped_s8_u4_prefill_runtime.cpp:231-346)
+
+Errors: invalid arguments raise ``ValueError``/``TypeError`` before launch;
+a failing C call raises ``AimaError``.  Out-of-range or duplicated expert ids
+are flagged in the workspace error word on the device (the reference throws
+``std::out_of_range`` / ``runtime_error``); ``Workspace.check()`` reads it.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import MoeLayerC, call, size_query
+from .layout import MoeLayerWeights, U4Weight
+
+MIN_WEIGHT_SUM = 6.103515625e-5  # gguf_loader.cpp:5665
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _require_cuda(*tensors: torch.Tensor) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError("tensors must live on the GPU (no CPU path)")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+class Workspace:
+    """Caller-owned scratch for the entry points that need it (grown on demand)."""
+
+    def __init__(self, device=None):
+        self.device = torch.device("cuda") if device is None else torch.device(device)
+        self.buf: Optional[torch.Tensor] = None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            if self.buf.data_ptr() % 256:
+                raise RuntimeError("workspace allocation is not 256-byte aligned")
+        return self.buf
+
+    def error_bits(self) -> int:
+        """Read and clear the device error word (synchronizes the stream)."""
+        if self.buf is None:
+            return 0
+        out = C.c_uint32(0)
+        call("aima_workspace_error", self.buf.data_ptr(), C.byref(out), _stream())
+        return int(out.value)
+
+    def check(self) -> None:
+        bits = self.error_bits()
+        if bits & _lib.AIMA_DEVERR_EXPERT_RANGE:
+            raise IndexError("expert id out of range")
+        if bits & _lib.AIMA_DEVERR_EXPERT_DUPLICATE:
+            raise ValueError("expert id duplicated within a token")
+
+
+_default_ws: dict = {}
+
+
+def _ws(ws: Optional[Workspace], device) -> Workspace:
+    if ws is not None:
+        return ws
+    key = str(device)
+    if key not in _default_ws:
+        _default_ws[key] = Workspace(device)
+    return _default_ws[key]
+
+
+# ---------------------------------------------------------------------------
+# U4 matrix ops
+# ---------------------------------------------------------------------------
+
+def u4_dequant(w: U4Weight) -> torch.Tensor:
+    """Exact dequantization f32(q - z) * f32(s) -> float32 [experts*rows, k]."""
+    _require_cuda(w.qweight)
+    n = w.experts * w.rows
+    out = torch.empty((n, w.k), dtype=torch.float32, device=w.qweight.device)
+    call("aima_u4_dequant", w.qweight.data_ptr(), w.scale.data_ptr(), w.zp.data_ptr(), n, w.k,
+         w.group, out.data_ptr(), _stream())
+    return out
+
+
+def matvec_u4(x: torch.Tensor, w: U4Weight, out_dtype=torch.float16) -> torch.Tensor:
+    """y = W x for a batch-1 float16 activation x [k]; f32 accumulate."""
+    _require_cuda(x, w.qweight)
+    if x.dtype != torch.float16 or x.numel() != w.k or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float16 vector of length k")
+    if out_dtype not in (torch.float16, torch.float32):
+        raise ValueError("out_dtype must be float16 or float32")
+    n = w.experts * w.rows
+    y = torch.empty(n, dtype=out_dtype, device=x.device)
+    call("aima_u4_matvec", x.data_ptr(), w.qweight.data_ptr(), w.scale.data_ptr(),
+         w.zp.data_ptr(), n, w.k, w.group, y.data_ptr(),
+         _lib.AIMA_OUT_F32 if out_dtype == torch.float32 else _lib.AIMA_OUT_F16, _stream())
+    return y
+
+
+def apply_rms_norm(x: torch.Tensor, weight: torch.Tensor, epsilon: float) -> torch.Tensor:
+    """Row-wise RMSNorm of float16 x [rows, hidden] with float32 weight -> float16."""
+    _require_cuda(x, weight)
+    if x.dtype != torch.float16 or weight.dtype != torch.float32:
+        raise TypeError("x must be float16 and weight float32")
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    if weight.numel() != x2.shape[1]:
+        raise ValueError("RMSNorm input and weight sizes differ")
+    out = torch.empty_like(x2)
+    call("aima_rmsnorm", x2.data_ptr(), weight.data_ptr(), x2.shape[0], x2.shape[1],
+         float(epsilon), out.data_ptr(), _stream())
+    return out.reshape(x.shape)
+
+
+def select_router_topk(logits: torch.Tensor, expert_used_count: int = 8,
+                       min_weight_sum: float = MIN_WEIGHT_SUM):
+    """Router logits float32 [..., E] -> (ids int32 [..., k], weights float32 [..., k])."""
+    _require_cuda(logits)
+    if logits.dtype != torch.float32:
+        raise TypeError("router logits must be float32")
+    E = logits.shape[-1]
+    l2 = logits.reshape(-1, E).contiguous()
+    k = int(expert_used_count)
+    if k <= 0 or k > E:
+        raise ValueError("top-k count must be in [1, experts]")
+    ids = torch.empty((l2.shape[0], k), dtype=torch.int32, device=logits.device)
+    w = torch.empty((l2.shape[0], k), dtype=torch.float32, device=logits.device)
+    call("aima_router_topk", l2.data_ptr(), l2.shape[0], E, k, float(min_weight_sum),
+         ids.data_ptr(), w.data_ptr(), _stream())
+    return ids.reshape(*logits.shape[:-1], k), w.reshape(*logits.shape[:-1], k)
+
+
+# ---------------------------------------------------------------------------
+# MoE FFN
+# ---------------------------------------------------------------------------
+
+def _check_route(ids: torch.Tensor, w: torch.Tensor, rows: int) -> int:
+    if ids.dtype != torch.int32 or w.dtype != torch.float32:
+        raise TypeError("expert ids must be int32 and weights float32")
+    if ids.shape != w.shape or ids.numel() % max(rows, 1):
+        raise ValueError("expert ids and weights must have matching [rows, k] shapes")
+    if not ids.is_contiguous() or not w.is_contiguous():
+        raise ValueError("expert ids and weights must be contiguous")
+    return ids.numel() // max(rows, 1)
+
+
+def run_moe_ffn_layer(layer: MoeLayerWeights, x: torch.Tensor, ids: torch.Tensor,
+                      weights: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                      ws: Optional[Workspace] = None) -> torch.Tensor:
+    """One token: f16(residual + sum_r w_r down_r(swiglu(gate_up_r x)) + shared)."""
+    _require_cuda(x, ids, weights, residual)
+    H = layer.hidden
+    if x.dtype != torch.float16 or x.numel() != H or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float16 [hidden] vector")
+    if residual is not None and (residual.dtype != torch.float16 or residual.numel() != H):
+        raise ValueError("residual must be float16 [hidden]")
+    k = _check_route(ids, weights, 1)
+    lc = layer.c()
+    ws = _ws(ws, x.device)
+    buf = ws.get(size_query("aima_moe_decode_workspace_size", C.byref(lc), k))
+    out = torch.empty(H, dtype=torch.float16, device=x.device)
+    call("aima_moe_ffn_decode", C.byref(lc), x.data_ptr(), _ptr(residual), ids.data_ptr(),
+         weights.data_ptr(), k, out.data_ptr(), buf.data_ptr(), buf.numel(), _stream())
+    return out
+
+
+def moe_decode_gate_up(layer: MoeLayerWeights, x: torch.Tensor, ids: torch.Tensor,
+                       act: Optional[torch.Tensor] = None,
+                       sigma: Optional[torch.Tensor] = None,
+                       error_word: Optional[torch.Tensor] = None, layer_c=None):
+    """Decode phase 1: SwiGLU activations f16 [k+1, I] (shared expert last) and
+    the shared gate sigmoid (float32 [1])."""
+    _require_cuda(x, ids)
+    k = ids.numel()
+    dev = x.device
+    if act is None:
+        act = torch.empty((k + 1, layer.inter), dtype=torch.float16, device=dev)
+    if sigma is None:
+        sigma = torch.empty(1, dtype=torch.float32, device=dev)
+    if error_word is None:
+        error_word = torch.zeros(1, dtype=torch.int32, device=dev)
+    lc = layer.c() if layer_c is None else layer_c
+    call("aima_moe_decode_gate_up", C.byref(lc), x.data_ptr(), ids.data_ptr(), k,
+         act.data_ptr(), sigma.data_ptr(), error_word.data_ptr(), _stream())
+    return act, sigma
+
+
+def moe_decode_down(layer: MoeLayerWeights, act: torch.Tensor, sigma: torch.Tensor,
+                    ids: torch.Tensor, weights: torch.Tensor,
+                    residual: Optional[torch.Tensor] = None,
+                    out: Optional[torch.Tensor] = None, layer_c=None) -> torch.Tensor:
+    """Decode phase 2: f16(residual + sum_r w_r down_r act_r + sigma * shared)."""
+    _require_cuda(act, sigma, ids, weights, residual)
+    k = _check_route(ids, weights, 1)
+    if out is None:
+        out = torch.empty(layer.hidden, dtype=torch.float16, device=act.device)
+    lc = layer.c() if layer_c is None else layer_c
+    call("aima_moe_decode_down", C.byref(lc), act.data_ptr(), sigma.data_ptr(), ids.data_ptr(),
+         weights.data_ptr(), k, _ptr(residual), out.data_ptr(), _stream())
+    return out
+
+
+def grouped_moe_prefill(layer: MoeLayerWeights, x: torch.Tensor, ids: torch.Tensor,
+                        weights: torch.Tensor, residual: Optional[torch.Tensor] = None,
+                        ws: Optional[Workspace] = None) -> torch.Tensor:
+    """T tokens: x float16 [T, H], ids int32 [T, k], weights float32 [T, k] -> f16 [T, H]."""
+    _require_cuda(x, ids, weights, residual)
+    if x.dtype != torch.float16 or x.dim() != 2 or x.shape[1] != layer.hidden:
+        raise ValueError("x must be float16 [tokens, hidden]")
+    x = x.contiguous()
+    T = x.shape[0]
+    k = _check_route(ids, weights, T)
+    if residual is not None:
+        if residual.shape != x.shape or residual.dtype != torch.float16:
+            raise ValueError("residual must match x")
+        residual = residual.contiguous()
+    lc = layer.c()
+    ws = _ws(ws, x.device)
+    buf = ws.get(size_query("aima_moe_prefill_workspace_size", C.byref(lc), T, k))
+    out = torch.empty_like(x)
+    call("aima_moe_grouped_prefill", C.byref(lc), x.data_ptr(), _ptr(residual), T,
+         ids.data_ptr(), weights.data_ptr(), k, out.data_ptr(), buf.data_ptr(), buf.numel(),
+         _stream())
+    return out
+
+
+def build_grouped_schedule(ids: torch.Tensor, router_weights: torch.Tensor, experts: int,
+                           ws: Optional[Workspace] = None) -> dict:
+    """Device BuildGroupedSchedule: offsets [E], token_map/inverse_map/compact_weights [T*k]."""
+    _require_cuda(ids, router_weights)
+    if ids.dim() != 2:
+        raise ValueError("ids must be [tokens, k]")
+    T, k = ids.shape
+    _check_route(ids, router_weights, T)
+    dev = ids.device
+    A = T * k
+    ws = _ws(ws, dev)
+    buf = ws.get(size_query("aima_grouped_schedule_workspace_size", T, k, experts))
+    out = {"offsets": torch.empty(experts, dtype=torch.int32, device=dev),
+           "token_map": torch.empty(A, dtype=torch.int32, device=dev),
+           "inverse_map": torch.empty(A, dtype=torch.int32, device=dev),
+           "compact_weights": torch.empty(A, dtype=torch.float32, device=dev)}
+    call("aima_grouped_schedule", ids.data_ptr(), router_weights.data_ptr(), T, k, experts,
+         out["offsets"].data_ptr(), out["token_map"].data_ptr(), out["inverse_map"].data_ptr(),
+         out["compact_weights"].data_ptr(), buf.data_ptr(), buf.numel(), _stream())
+    return out
+
+
+def _layers_c(layers: Sequence[MoeLayerWeights]):
+    arr = (MoeLayerC * len(layers))()
+    for i, l in enumerate(layers):
+        if l.norm_weight is None:
+            raise ValueError("stack layers need norm_weight")
+        arr[i] = l.c()
+    return arr
+
+
+def moe_stack_decode(layers: Sequence[MoeLayerWeights], residual: torch.Tensor,
+                     ids: torch.Tensor, weights: torch.Tensor, epsilon: float = 1e-6,
+                     ws: Optional[Workspace] = None, out: Optional[torch.Tensor] = None,
+                     layers_c=None) -> torch.Tensor:
+    """len(layers) layers for one token; ids/weights [L, k]; residual f16 [H]."""
+    _require_cuda(residual, ids, weights)
+    L = len(layers)
+    H = layers[0].hidden
+    if residual.dtype != torch.float16 or residual.numel() != H:
+        raise ValueError("residual must be float16 [hidden]")
+    k = _check_route(ids, weights, L)
+    arr = _layers_c(layers) if layers_c is None else layers_c
+    ws = _ws(ws, residual.device)
+    buf = ws.get(size_query("aima_moe_decode_workspace_size", C.byref(arr[0]), k))
+    if out is None:
+        out = torch.empty(H, dtype=torch.float16, device=residual.device)
+    call("aima_moe_stack_decode", arr, L, float(epsilon), residual.data_ptr(), ids.data_ptr(),
+         weights.data_ptr(), k, out.data_ptr(), buf.data_ptr(), buf.numel(), _stream())
+    return out
+
+
+def moe_stack_prefill(layers: Sequence[MoeLayerWeights], x: torch.Tensor, ids: torch.Tensor,
+                      weights: torch.Tensor, epsilon: float = 1e-6,
+                      ws: Optional[Workspace] = None, out: Optional[torch.Tensor] = None,
+                      layers_c=None) -> torch.Tensor:
+    """len(layers) layers for T tokens; x f16 [T, H]; ids/weights [L, T, k]."""
+    _require_cuda(x, ids, weights)
+    L = len(layers)
+    if x.dtype != torch.float16 or x.dim() != 2:
+        raise ValueError("x must be float16 [tokens, hidden]")
+    x = x.contiguous()
+    T = x.shape[0]
+    if ids.dim() != 3 or ids.shape[0] != L or ids.shape[1] != T:
+        raise ValueError("ids must be [layers, tokens, k]")
+    k = ids.shape[2]
+    _check_route(ids, weights, L * T)
+    arr = _layers_c(layers) if layers_c is None else layers_c
+    ws = _ws(ws, x.device)
+    buf = ws.get(size_query("aima_moe_stack_prefill_workspace_size", C.byref(arr[0]), T, k))
+    if out is None:
+        out = torch.empty_like(x)
+    call("aima_moe_stack_prefill", arr, L, float(epsilon), x.data_ptr(), T, ids.data_ptr(),
+         weights.data_ptr(), k, out.data_ptr(), buf.data_ptr(), buf.numel(), _stream())
+    return out

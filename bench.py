@@ -1,0 +1,379 @@
+#!/usr/bin/env python3
+"""Benchmark of the U4 MoE hot path on one MI355X.
+
+Headline workload (BASELINE.json metric "MoE-FFN decode us/token + HBM GB/s
+%peak; grouped prefill tok/s at T=2048"): the 40-layer MoE FFN stack of
+config 4 (40 x 256 routed experts + 40 shared experts resident, hidden 2048,
+expert intermediate 512, group-128 U4, ~17 GB), one batch-1 decode step per
+"step": router top-8 from seeded logits for all 40 layers, then RMSNorm ->
+MoE FFN -> residual through every layer.  ``value`` is us per decode token.
+
+The same line carries
+* ``roofline``: the dominant decode kernel (routed+shared gate/up + SwiGLU),
+  algorithmic bytes per launch / its event-timed average launch time;
+* ``prefill``: grouped prefill of one layer at T=2048 (config 2, Zipf(1.1)
+  skewed routing) in tok/s and MFMA fraction, and the 40-layer T=16384 chunk
+  (config 4b);
+* ``configs``: config 0 (U4 matvec), 1 (one decode layer), 3 (LM-head matvec);
+* ``cpu_baseline``: the CPU oracle (restatement of the reference CPU path) on
+  this host's cores for a bounded sample of the same decode workload.
+Inputs are synthetic (seeded), weights random-init, all resident in HBM
+before timing.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+H, I, E, K_TOP, GROUP, LAYERS = 2048, 512, 256, 8, 128, 40
+EPS = 1e-6
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def u4_bytes(rows, k, group=GROUP):
+    return rows * k // 2 + rows * (k // group) * 2 + rows * (k // group) // 2
+
+
+GATEUP_EXPERT_B = u4_bytes(2 * I, H)   # 1,089,536
+DOWN_EXPERT_B = u4_bytes(H, I)         # 544,768
+EXPERT_B = GATEUP_EXPERT_B + DOWN_EXPERT_B  # 1,634,304
+
+
+def timed(torch, fn, iters, warmup=2):
+    for _ in range(warmup):
+        fn()
+    stream = torch.cuda.current_stream()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(iters):
+        fn()
+    b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) * 1e3 / iters  # us per call
+
+
+def graphed(torch, fn):
+    """Capture fn into a HIP graph (after a warm run); returns replay callable."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g.replay
+
+
+def cpu_baseline(torch, pkg, oracle, layers, x, ids, w, budget_s=12.0):
+    """The oracle's threaded decode (row-parallel matvecs, the reference CPU
+    pattern) through all 40 layers for the decode token, repeated within a
+    time budget.  Only the experts the token selects are copied to the host."""
+    from tests.helpers import f16_bits, u4_to_oracle
+
+    threads = min(16, os.cpu_count() or 1)
+    ids_np = ids.cpu().numpy()
+    w_np = w.cpu().numpy()
+    host = []
+    for L, layer in enumerate(layers):
+        idx = torch.as_tensor(ids_np[L].astype("int64"), device=layer.gate_up.qweight.device)
+
+        def pick(t):
+            return u4_to_oracle(type(t)(t.qweight.index_select(0, idx).contiguous(),
+                                        t.scale.index_select(0, idx).contiguous(),
+                                        t.zp.index_select(0, idx).contiguous(),
+                                        t.rows, t.k, t.group))
+
+        host.append((oracle.MoeWeights(pick(layer.gate_up), pick(layer.down),
+                                       u4_to_oracle(layer.shared_gate_up),
+                                       u4_to_oracle(layer.shared_down),
+                                       f16_bits(layer.shared_gate_vec)),
+                     layer.norm_weight.cpu().numpy()))
+    import numpy as np
+
+    local_ids = np.arange(K_TOP, dtype=np.int32)
+    x_bits = f16_bits(x)
+
+    def one_token():
+        r = x_bits
+        for L, (mw, nw) in enumerate(host):
+            rf = oracle.f16_values(r)
+            h = oracle.f16_values(oracle.float_to_half(oracle.rms_norm(rf, nw, EPS)))
+            o = oracle.moe_ffn_decode_threaded(mw, h, local_ids, w_np[L], residual=rf,
+                                               threads=threads)
+            r = oracle.float_to_half(o)
+        return r
+
+    one_token()  # warm
+    samples = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(samples) < 3:
+        t0 = time.perf_counter()
+        one_token()
+        samples.append((time.perf_counter() - t0) * 1e6)
+    samples.sort()
+    return {"value": samples[len(samples) // 2], "unit": "us/token", "cores": threads,
+            "kind": "port", "min": samples[0], "mean": sum(samples) / len(samples),
+            "sample": f"{len(samples)} decode tokens through all 40 layers (8 routed + shared "
+                      f"expert per layer, U4 dequant + sequential f32 dots, row-parallel over "
+                      f"{threads} threads); median reported",
+            "host_cpu": _cpu_model()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="only the headline decode step (for profiling runs)")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus > 1 or world > 1:
+        print("bench.py measures one GPU: the batch-1 decode and grouped prefill path here "
+              "is single-device (multi-GPU sharding is a design note, not a build target); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__
+
+    pkg = __graft_entry__.load_package()
+    from aima_u4moe import ops, synth  # noqa: E402
+
+    dev = torch.device("cuda:0")
+    log(f"device {torch.cuda.get_device_name(0)}; building 40-layer stack")
+    t0 = time.perf_counter()
+    layers = [synth.moe_layer(hidden=H, inter=I, experts=E, group=GROUP, seed=4000 + l,
+                              device=dev) for l in range(LAYERS)]
+    layers_c = ops._layers_c(layers)
+    torch.cuda.synchronize()
+    log(f"stack resident in {time.perf_counter() - t0:.1f}s, "
+        f"{sum(l.gate_up.nbytes + l.down.nbytes + l.shared_bytes() for l in layers) / 1e9:.2f} GB")
+
+    # ------------------------------------------------------------------ decode
+    x = synth.activations(1, H, 41, dev)[0].contiguous()
+    logits = torch.stack([synth.router_logits(1, E, 1041 + l, dev)[0] for l in range(LAYERS)])
+    ws = ops.Workspace(dev)
+    out = torch.empty(H, dtype=torch.float16, device=dev)
+    ids_buf = torch.empty((LAYERS, K_TOP), dtype=torch.int32, device=dev)
+    w_buf = torch.empty((LAYERS, K_TOP), dtype=torch.float32, device=dev)
+    lib = pkg._lib
+
+    def decode_step():
+        lib.call("aima_router_topk", logits.data_ptr(), LAYERS, E, K_TOP,
+                 ops.MIN_WEIGHT_SUM, ids_buf.data_ptr(), w_buf.data_ptr(), ops._stream())
+        ops.moe_stack_decode(layers, x, ids_buf, w_buf, EPS, ws=ws, out=out, layers_c=layers_c)
+
+    eager_us = timed(torch, decode_step, args.steps, warmup=args.warmup)
+    log(f"decode eager: {eager_us:.1f} us/token")
+    replay = graphed(torch, decode_step)
+    graph_us = timed(torch, replay, args.steps, warmup=args.warmup)
+    log(f"decode graph: {graph_us:.1f} us/token")
+    ws.check()
+    step_us = min(eager_us, graph_us)
+    decode_mode = "hip-graph" if graph_us <= eager_us else "eager"
+    torch.cuda.synchronize()
+    ids_np = ids_buf.cpu().numpy()
+    n_unique = sum(len(set(r)) for r in ids_np)
+    weight_bytes = LAYERS * (K_TOP * EXPERT_B + EXPERT_B)  # 8 routed + shared per layer
+    act_bytes = LAYERS * (H * 2 * 3 + H * 4 + (K_TOP + 1) * I * 2 * 2 + H * 2)
+    decode_gbs = (weight_bytes + act_bytes) / step_us / 1e3
+
+    # dominant kernel: routed+shared gate/up + SwiGLU, one launch per layer
+    act = torch.empty((K_TOP + 1, I), dtype=torch.float16, device=dev)
+    sig = torch.empty(1, dtype=torch.float32, device=dev)
+    errw = torch.zeros(1, dtype=torch.int32, device=dev)
+    hs = [synth.activations(1, H, 7000 + l, dev)[0].contiguous() for l in range(LAYERS)]
+    id_rows = [ids_buf[l].contiguous() for l in range(LAYERS)]
+
+    def gate_up_all():
+        for l in range(LAYERS):
+            ops.moe_decode_gate_up(layers[l], hs[l], id_rows[l], act=act, sigma=sig,
+                                   error_word=errw, layer_c=layers_c[l])
+
+    g_replay = graphed(torch, gate_up_all)
+    reps = max(5, args.steps // 4)
+    per_launch_us = timed(torch, g_replay, reps, warmup=3) / LAYERS
+    gu_bytes = (K_TOP + 1) * GATEUP_EXPERT_B + H * 2 * 2 + (K_TOP + 1) * I * 2
+    achieved = gu_bytes / per_launch_us / 1e3
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "decode_gateup_kernel<64>", "bytes_per_launch": gu_bytes,
+                "avg_launch_us": round(per_launch_us, 3)}
+    log(f"gate/up kernel: {per_launch_us:.2f} us/launch, {achieved:.0f} GB/s")
+
+    result = {
+        "metric": "MoE-FFN decode us/token + HBM GB/s %peak; grouped prefill tok/s at T=2048",
+        "value": round(step_us, 2), "unit": "us/token", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(step_us / 1e3, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "u4xf16",
+        "data": "synthetic (seeded U4 weights, f16 activations, f32 router logits)",
+        "config": {"workload": "config4a: 40-layer MoE FFN decode step, batch 1, top-8/256 + "
+                               "shared expert, hidden 2048, inter 512, U4 group 128",
+                   "layers": LAYERS, "experts": E, "top_k": K_TOP, "hidden": H, "inter": I,
+                   "group": GROUP, "parallelism": "single-gpu"},
+        "decode": {"us_per_token": round(step_us, 2), "eager_us": round(eager_us, 2),
+                   "graph_us": round(graph_us, 2), "mode": decode_mode,
+                   "algorithmic_bytes": weight_bytes + act_bytes,
+                   "hbm_gbs": round(decode_gbs, 1),
+                   "hbm_frac": round(decode_gbs / HBM_PEAK_GBS, 4),
+                   "unique_experts_per_step": int(n_unique)},
+        "roofline": roofline,
+    }
+
+    if not args.no_extras:
+        result["prefill"] = prefill_bench(torch, pkg, ops, synth, layers, layers_c, dev)
+        result["configs"] = matvec_bench(torch, ops, synth, layers, layers_c, dev, ids_buf,
+                                         w_buf)
+
+    if not args.no_cpu_baseline:
+        import oracle
+
+        log("cpu baseline (oracle, 40-layer decode token)")
+        result["cpu_baseline"] = cpu_baseline(torch, pkg, oracle, layers, x, ids_buf, w_buf)
+    print(json.dumps(result), flush=True)
+
+
+def prefill_bench(torch, pkg, ops, synth, layers, layers_c, dev):
+    out = {}
+    # config 2: one layer, T=2048, Zipf(1.1)-skewed routing
+    T = 2048
+    layer = layers[0]
+    x = synth.activations(T, H, 2, dev)
+    ids, w = ops.select_router_topk(synth.router_logits(T, E, 3, dev, zipf_s=1.1), K_TOP)
+    ws = ops.Workspace(dev)
+    o = torch.empty_like(x)
+
+    def run():
+        lc = layers_c[0]
+        import ctypes as C
+        buf = ws.get(pkg._lib.size_query("aima_moe_prefill_workspace_size", C.byref(lc), T,
+                                         K_TOP))
+        pkg._lib.call("aima_moe_grouped_prefill", C.byref(lc), x.data_ptr(), None, T,
+                      ids.data_ptr(), w.data_ptr(), K_TOP, o.data_ptr(), buf.data_ptr(),
+                      buf.numel(), ops._stream())
+
+    us = timed(torch, run, 50, warmup=5)
+    ws.check()
+    flops = (T * K_TOP + T) * 2 * (H * 2 * I + I * H)
+    counts = torch.bincount(ids.reshape(-1).long(), minlength=E)
+    active = int((counts > 0).sum())
+    wbytes = active * EXPERT_B + EXPERT_B
+    tf = flops / us / 1e6
+    out["config2_T2048"] = {"us": round(us, 2), "tok_s": round(T / us * 1e6, 1),
+                            "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                            "hbm_weight_gbs": round(wbytes / us / 1e3, 1),
+                            "active_experts": active, "max_group": int(counts.max()),
+                            "flops": flops}
+    log(f"prefill T=2048: {us:.1f} us, {T / us * 1e6:.0f} tok/s, {tf:.1f} TFLOP/s")
+    # config 4b: 40 layers, T=16384
+    T = 16384
+    x = synth.activations(T, H, 43, dev)
+    logits = torch.stack([synth.router_logits(T, E, 2044 + l, dev) for l in range(LAYERS)])
+    ids, w = ops.select_router_topk(logits, K_TOP)
+    del logits
+    ws2 = ops.Workspace(dev)
+    o = torch.empty_like(x)
+
+    def run4b():
+        ops.moe_stack_prefill(layers, x, ids, w, EPS, ws=ws2, out=o, layers_c=layers_c)
+
+    us = timed(torch, run4b, 3, warmup=1)
+    ws2.check()
+    flops = LAYERS * (T * K_TOP + T) * 2 * (H * 2 * I + I * H)
+    tf = flops / us / 1e6
+    out["config4b_T16384_40L"] = {"us": round(us, 1), "tok_s": round(T / us * 1e6, 1),
+                                  "tflops": round(tf, 2),
+                                  "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                                  "flops": flops}
+    log(f"prefill 40L T=16384: {us / 1e3:.2f} ms, {tf:.1f} TFLOP/s")
+    return out
+
+
+def matvec_bench(torch, ops, synth, layers, layers_c, dev, ids_buf, w_buf):
+    out = {}
+    # config 0: K=2048, N=4096 over 64 rotating weight copies (~280 MB, past the caches)
+    gen = synth.generator(0, dev)
+    copies = [synth.u4_weight(1, 4096, 2048, GROUP, gen, dev) for _ in range(64)]
+    x = synth.activations(1, 2048, 0, dev)[0].contiguous()
+    y = torch.empty(4096, dtype=torch.float16, device=dev)
+    import ctypes as C
+    lib = ops._lib
+
+    def mv_all():
+        for wgt in copies:
+            lib.call("aima_u4_matvec", x.data_ptr(), wgt.qweight.data_ptr(),
+                     wgt.scale.data_ptr(), wgt.zp.data_ptr(), 4096, 2048, GROUP, y.data_ptr(),
+                     0, ops._stream())
+
+    rep = graphed(torch, mv_all)
+    us = timed(torch, rep, 20, warmup=2) / len(copies)
+    b0 = u4_bytes(4096, 2048) + 2048 * 2 + 4096 * 2
+    out["config0_matvec_K2048_N4096"] = {"us": round(us, 3), "gbs": round(b0 / us / 1e3, 1),
+                                         "hbm_frac": round(b0 / us / 1e3 / HBM_PEAK_GBS, 4),
+                                         "bytes": b0}
+    del copies
+    # config 1: one decode layer, cycling over the 40 resident layers (cache-cold)
+    ws = ops.Workspace(dev)
+    o = torch.empty(H, dtype=torch.float16, device=dev)
+    res = synth.activations(1, H, 5, dev)[0].contiguous()
+    rows = [(ids_buf[l].contiguous(), w_buf[l].contiguous()) for l in range(LAYERS)]
+    buf = ws.get(ops.size_query("aima_moe_decode_workspace_size", C.byref(layers_c[0]), K_TOP))
+
+    def layer_all():
+        for l in range(LAYERS):
+            lib.call("aima_moe_ffn_decode", C.byref(layers_c[l]), x.data_ptr(), res.data_ptr(),
+                     rows[l][0].data_ptr(), rows[l][1].data_ptr(), K_TOP, o.data_ptr(),
+                     buf.data_ptr(), buf.numel(), ops._stream())
+
+    rep = graphed(torch, layer_all)
+    us = timed(torch, rep, 20, warmup=2) / LAYERS
+    b1 = (K_TOP + 1) * EXPERT_B
+    out["config1_decode_layer"] = {"us": round(us, 3), "gbs": round(b1 / us / 1e3, 1),
+                                   "hbm_frac": round(b1 / us / 1e3 / HBM_PEAK_GBS, 4),
+                                   "weight_bytes": b1}
+    # config 3: LM-head-sized matvec, K=2048, N=248320, f32 logits
+    wl = synth.u4_weight(1, 248320, 2048, GROUP, synth.generator(3, dev), dev)
+    xl = synth.activations(1, 2048, 3, dev)[0].contiguous()
+    us = timed(torch, lambda: ops.matvec_u4(xl, wl, out_dtype=torch.float32), 50, warmup=5)
+    b3 = u4_bytes(248320, 2048) + 2048 * 2 + 248320 * 4
+    out["config3_lm_head_N248320"] = {"us": round(us, 2), "gbs": round(b3 / us / 1e3, 1),
+                                      "hbm_frac": round(b3 / us / 1e3 / HBM_PEAK_GBS, 4),
+                                      "bytes": b3}
+    log(f"config0 {out['config0_matvec_K2048_N4096']['us']} us, config1 "
+        f"{out['config1_decode_layer']['us']} us, config3 {out['config3_lm_head_N248320']['us']} us")
+    return out
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,243 @@
+/*
+ * aima_u4moe.h -- C ABI of the MI355X U4 MoE expert hot path.
+ *
+ * One shared library, libaima_u4moe.so, hand-written HIP for gfx950.  Every
+ * entry point:
+ *   - takes caller-owned DEVICE pointers and plain sizes (no framework types);
+ *   - enqueues asynchronously on `stream` (a hipStream_t, NULL = default
+ *     stream) and never synchronizes the host;
+ *   - returns AIMA_OK or a negative AIMA_E_* code, with a thread-local message
+ *     in aima_last_error(); nothing is thrown across the ABI;
+ *   - is re-entrant across distinct streams when given distinct workspaces.
+ * Entry points that need scratch memory take a caller-owned workspace whose
+ * size the matching *_workspace_size function reports; they allocate nothing.
+ *
+ * U4 group-quantized matrix W[N][K] (the boundary layout, from the OpenVINO IR
+ * constants traced by tools/intel_qwen36_openvino_fixed_fc.py:107-144,241-265
+ * and consumed by engine/openvino/custom/iq36_fixed_fc_multi_output.cl:118-127):
+ *   qweight  u8 [N][K/2]     low nibble = even k, high nibble = odd k
+ *   scale    f16[N][K/g]     row-major per (row, group)
+ *   zp       u4 over the flat [N*(K/g)] index, two per byte, low nibble = even
+ *   w[n][k] = f32(q - z) * f32(s)
+ * Expert stacks are E such matrices back to back.  A routed gate/up stack has
+ * 2*I rows per expert: rows 0..I-1 gate, I..2I-1 up (the CPU reference's
+ * convention, engine/src/gguf_loader.cpp:4654-4660).
+ *
+ * f16 values travel as uint16_t bit patterns.
+ */
+#ifndef AIMA_U4MOE_H_
+#define AIMA_U4MOE_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AIMA_OK 0
+#define AIMA_E_INVALID (-1)   /* bad size, shape, alignment or null pointer */
+#define AIMA_E_RANGE (-2)     /* expert id out of range / duplicated (device flag) */
+#define AIMA_E_HIP (-3)       /* a HIP runtime call failed */
+#define AIMA_E_WORKSPACE (-4) /* workspace missing or too small */
+#define AIMA_E_UNSUPPORTED (-5) /* shape outside what the kernels implement */
+
+/* Bits of the device error word kept at the start of every workspace.  They
+ * mirror the reference device-schedule error bits (1 = out of range,
+ * 2 = duplicated within a token; grouped_s8_u4_f16_contribution_moe.cl:38-53). */
+#define AIMA_DEVERR_EXPERT_RANGE 1u
+#define AIMA_DEVERR_EXPERT_DUPLICATE 2u
+
+#define AIMA_OUT_F16 0
+#define AIMA_OUT_F32 1
+
+/* Device pointers of one U4 matrix or expert stack. */
+typedef struct aima_u4_tensor {
+  const uint8_t* qweight;
+  const uint16_t* scale;
+  const uint8_t* zp;
+} aima_u4_tensor;
+
+/* One MoE FFN layer, all device pointers.
+ *   gate_up        E x [2*inter][hidden]
+ *   down           E x [hidden][inter]
+ *   shared_gate_up 1 x [2*shared_inter][hidden]
+ *   shared_down    1 x [hidden][shared_inter]
+ *   shared_gate_vec f16[hidden]; the shared expert is scaled by
+ *                   sigmoid(dot(shared_gate_vec, h))
+ *   norm_weight    f32[hidden] RMSNorm weight applied before the layer by the
+ *                   stack entry points (may be NULL for single-layer calls). */
+typedef struct aima_moe_layer {
+  aima_u4_tensor gate_up;
+  aima_u4_tensor down;
+  aima_u4_tensor shared_gate_up;
+  aima_u4_tensor shared_down;
+  const uint16_t* shared_gate_vec;
+  const float* norm_weight;
+  int32_t hidden;
+  int32_t inter;
+  int32_t shared_inter;
+  int32_t experts;
+  int32_t group;
+} aima_moe_layer;
+
+/* Thread-local description of the last failure on this thread. */
+const char* aima_last_error(void);
+
+/* Library ABI version (major*100 + minor). */
+int aima_version(void);
+
+/* Exact dequantization out[n][k] = f32(q - z) * f32(s) (bit-exact with the
+ * OpenVINO decompression subgraph Convert -> Subtract(zp) -> Multiply(scale),
+ * tools/intel_qwen36_openvino_fixed_fc.py:111-119).  K % group == 0,
+ * group % 32 == 0. */
+int aima_u4_dequant(const uint8_t* qweight, const uint16_t* scale,
+                    const uint8_t* zp, int64_t n, int64_t k, int32_t group,
+                    float* out, void* stream);
+
+/* Batch-1 U4 weight-only matvec y[n] = sum_k w[n][k] * x[k], f32 accumulate,
+ * output f16 (round to nearest even) or f32.  Replaces the U4 fixed-FC op
+ * iq36_fixed_fc1 (engine/openvino/custom/iq36_fixed_fc_multi_output.cl:32-40,
+ * arguments input, weight, out, scale, zp) and the CPU matvec_tensor
+ * (engine/include/intel_qwen36/gguf_loader.hpp:379-382).
+ * K = 32 * 2^j with 128 <= K <= 8192, group in {32,64,128,256}, 16-byte
+ * aligned qweight. */
+int aima_u4_matvec(const uint16_t* x, const uint8_t* qweight,
+                   const uint16_t* scale, const uint8_t* zp, int64_t n,
+                   int64_t k, int32_t group, void* y, int32_t out_dtype,
+                   void* stream);
+
+/* RMSNorm per row, out = f16(x * (1/sqrt(mean(x^2) + eps)) * weight) with f32
+ * arithmetic.  Replaces apply_rms_norm
+ * (engine/include/intel_qwen36/gguf_loader.hpp:355-357). */
+int aima_rmsnorm(const uint16_t* x, const float* weight, int64_t rows,
+                 int64_t hidden, float eps, uint16_t* out, void* stream);
+
+/* Router selection per token: softmax over `experts` logits (f64), top-k
+ * (value descending, lower id on ties), weights renormalized over the k by
+ * max(sum, min_weight_sum).  Replaces select_router_topk
+ * (engine/include/intel_qwen36/gguf_loader.hpp:371-373) and the device
+ * iq36_router_topk8_1024 (grouped_s8_u4_f16_contribution_moe.cl:222-291).
+ * experts <= 1024, k <= 16. */
+int aima_router_topk(const float* logits, int64_t tokens, int32_t experts,
+                     int32_t k, float min_weight_sum, int32_t* ids,
+                     float* weights, void* stream);
+
+/* Workspace bytes for aima_moe_ffn_decode / aima_moe_stack_decode. */
+int aima_moe_decode_workspace_size(const aima_moe_layer* layer, int32_t k,
+                                   size_t* bytes);
+
+/* One MoE FFN block for one token (batch-1 decode):
+ *   out = f16(residual + sum_r w[r] * down_{ids[r]}(swiglu(gate_up_{ids[r]} h))
+ *             + sigmoid(shared_gate_vec . h) * shared_down(swiglu(shared_gate_up h)))
+ * h = x (f16[hidden]); residual may be NULL (then it is 0); ids/weights are
+ * device arrays of k entries (the router's top-k output).  Replaces
+ * run_qwen36_moe_ffn_layer's expert part (gguf_loader.hpp:519-524,
+ * gguf_loader.cpp:5711-5780) and the decode runner
+ * RunResidentPackedQ4X8Expert8PlusSharedThenSwiGlu
+ * (engine/src/gpu_q4x8_matvec.cpp:3464-3664).  Invalid expert ids set
+ * AIMA_DEVERR_EXPERT_RANGE in the workspace error word and contribute 0. */
+int aima_moe_ffn_decode(const aima_moe_layer* layer, const uint16_t* x,
+                        const uint16_t* residual, const int32_t* ids,
+                        const float* weights, int32_t k, uint16_t* out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* The two launches of aima_moe_ffn_decode, separately.
+ * Gate/up: act[r][j] = f16(silu(g) * u) for the k routed experts (slot r =
+ * ids[r]) and the shared expert (slot k), act f16 [k+1][inter], plus the
+ * shared gate *shared_sigma = sigmoid(shared_gate_vec . x).  Replaces the
+ * decode runner's expert8-plus-shared gate/up matvec with the SwiGLU
+ * (engine/src/gpu_q4x8_matvec.cpp:3464-3664, kernels
+ * q4k_x8_matvec_rowlane_expert8_plus_shared_localq8 and ffn_moe_swiglu_f32,
+ * engine/gpu/opencl/q4x8_matvec.cl:1908-2008,2679-2694).  Invalid ids set
+ * AIMA_DEVERR_EXPERT_RANGE in *error_word. */
+int aima_moe_decode_gate_up(const aima_moe_layer* layer, const uint16_t* x,
+                            const int32_t* ids, int32_t k, uint16_t* act,
+                            float* shared_sigma, uint32_t* error_word,
+                            void* stream);
+
+/* Down + aggregate: out = f16(residual + sum_r weights[r] * down_{ids[r]} act[r]
+ * + shared_sigma * shared_down act[k]), rank order fixed, no atomics.
+ * Replaces the selected-down + FFN tail (q4s_group128_all_expert_down_topk8_plus_shared,
+ * ffn_moe_weighted_aggregate_f32, shared_expert_gate_apply_f32,
+ * ffn_output_add_f32, post_ffn_residual_add_f32;
+ * engine/gpu/opencl/q4x8_matvec.cl:1023-1052,4358-4418). */
+int aima_moe_decode_down(const aima_moe_layer* layer, const uint16_t* act,
+                         const float* shared_sigma, const int32_t* ids,
+                         const float* weights, int32_t k,
+                         const uint16_t* residual, uint16_t* out, void* stream);
+
+/* Workspace bytes for aima_moe_grouped_prefill / aima_moe_stack_prefill. */
+int aima_moe_prefill_workspace_size(const aima_moe_layer* layer,
+                                    int64_t tokens, int32_t k, size_t* bytes);
+
+/* Grouped MoE FFN over T tokens (prefill): tokens are sorted by expert on the
+ * device (stable by token), each expert runs a grouped gate/up GEMM with the
+ * SwiGLU epilogue and a grouped down GEMM scaled by the router weight on
+ * MFMA, and every token's output is the rank-ordered sum of its k
+ * contributions plus the sigmoid-gated shared expert (plus residual, if not
+ * NULL).  x, residual, out: f16 [T][hidden]; ids, weights: [T][k].
+ * Replaces GroupedS8U4PrefillRuntime::RunLayer
+ * (engine/include/intel_qwen36/grouped_s8_u4_prefill_runtime.hpp:148-150,
+ * top-k int32[T][8] + float[T*8] in, per-token routed sum out) and the
+ * OpenVINO MOE3GemmFusedCompressed op
+ * (engine/openvino/iq36-fixed-fc-moe-router-compat.patch:49-56).
+ * Requires shared_inter == inter, hidden % 128 == 0, inter % 128 == 0. */
+int aima_moe_grouped_prefill(const aima_moe_layer* layer, const uint16_t* x,
+                             const uint16_t* residual, int64_t tokens,
+                             const int32_t* ids, const float* weights,
+                             int32_t k, uint16_t* out, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/* Workspace bytes for aima_grouped_schedule. */
+int aima_grouped_schedule_workspace_size(int64_t tokens, int32_t k,
+                                         int32_t experts, size_t* bytes);
+
+/* The grouped schedule alone (the step the prefill runs first): a stable
+ * device counting sort of the T*k assignments by expert.  Outputs, all
+ * device arrays: offsets[E] = exclusive end row of each expert, token_map[A]
+ * = source token of each sorted row, inverse_map[A] = sorted row of each
+ * (token, rank), compact_weights[A] = router weight of each sorted row.
+ * Same results as the host BuildGroupedSchedule
+ * (engine/src/grouped_s8_u4_prefill_runtime.cpp:231-346: rows of one expert
+ * in (token, rank) order); out-of-range or duplicated ids set the workspace
+ * error word (the reference throws). */
+int aima_grouped_schedule(const int32_t* ids, const float* weights,
+                          int64_t tokens, int32_t k, int32_t experts,
+                          int32_t* offsets, int32_t* token_map,
+                          int32_t* inverse_map, float* compact_weights,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* n_layers MoE FFN layers for one token: r_0 = residual_in and for each
+ * layer L, h = f16(rmsnorm(r_L, layers[L].norm_weight, eps)),
+ * r_{L+1} = f16(r_L + ffn_L(h)).  ids/weights: [n_layers][k].  `layers` is a
+ * HOST array of layer descriptors.  out = r_{n_layers}. */
+int aima_moe_stack_decode(const aima_moe_layer* layers, int32_t n_layers,
+                          float eps, const uint16_t* residual_in,
+                          const int32_t* ids, const float* weights, int32_t k,
+                          uint16_t* out, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/* Workspace bytes for aima_moe_stack_prefill (one layer's prefill workspace
+ * plus the normalized activations). */
+int aima_moe_stack_prefill_workspace_size(const aima_moe_layer* layer,
+                                          int64_t tokens, int32_t k,
+                                          size_t* bytes);
+
+/* The same stack for T tokens: x_in, out f16 [T][hidden]; ids/weights
+ * [n_layers][T][k]. */
+int aima_moe_stack_prefill(const aima_moe_layer* layers, int32_t n_layers,
+                           float eps, const uint16_t* x_in, int64_t tokens,
+                           const int32_t* ids, const float* weights, int32_t k,
+                           uint16_t* out, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* Copy the device error word of a workspace to the host (synchronizes
+ * `stream`).  0 = no error; otherwise AIMA_DEVERR_* bits.  Clears it. */
+int aima_workspace_error(void* workspace, uint32_t* error_bits, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AIMA_U4MOE_H_ */

@@ -1,0 +1,133 @@
+"""The C-ABI library on a host without a GPU: it loads, exports every entry
+point the header declares, binds to torch's HIP runtime, and rejects bad
+arguments with the documented error codes before launching anything."""
+
+import ctypes as C
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "aima_u4moe.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\w[\w\s\*]*?\b(aima_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    names = declared_functions()
+    assert "aima_u4_matvec" in names and "aima_moe_grouped_prefill" in names
+    assert len(names) >= 16
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = pkg._lib.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert set(declared_functions()) == set(pkg._lib.SIGNATURES)
+
+
+def test_library_shares_torch_hip_runtime(pkg):
+    pkg._lib.lib()
+    maps = open("/proc/self/maps").read()
+    hip = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(hip) == 1, hip
+
+
+def test_version_and_error_paths(pkg):
+    L = pkg._lib.lib()
+    assert L.aima_version() == 100
+    rc = L.aima_u4_matvec(None, None, None, None, 4, 2048, 128, None, 0, None)
+    assert rc == pkg._lib.AIMA_E_INVALID
+    assert b"null pointer" in L.aima_last_error()
+    # fake but aligned device pointers: validation happens before any launch
+    p = C.c_void_p(1 << 20)
+    rc = L.aima_u4_matvec(p, p, p, p, 4, 3000, 128, p, 0, None)
+    assert rc == pkg._lib.AIMA_E_INVALID  # k not a multiple of group
+    rc = L.aima_u4_matvec(p, p, p, p, 4, 2048, 100, p, 0, None)
+    assert rc == pkg._lib.AIMA_E_INVALID  # bad group
+    rc = L.aima_u4_matvec(p, p, p, p, 4, 3072, 128, p, 0, None)
+    assert rc == pkg._lib.AIMA_E_UNSUPPORTED  # K not a power of two
+    rc = L.aima_u4_matvec(p, C.c_void_p((1 << 20) + 4), p, p, 4, 2048, 128, p, 0, None)
+    assert rc == pkg._lib.AIMA_E_INVALID  # misaligned qweight
+    rc = L.aima_router_topk(p, 4, 256, 17, 1e-4, p, p, None)
+    assert rc == pkg._lib.AIMA_E_INVALID  # k > 16
+
+
+def _fake_layer(pkg, H=2048, I=512, E=256, group=128):
+    p = 1 << 20
+    t = pkg._lib.U4TensorC(p, p, p)
+    return pkg._lib.MoeLayerC(t, t, t, t, p, p, H, I, I, E, group)
+
+
+def test_workspace_sizes(pkg):
+    L = pkg._lib
+    lc = _fake_layer(pkg)
+    dec = L.size_query("aima_moe_decode_workspace_size", C.byref(lc), 8)
+    assert dec >= 256 + 9 * 512 * 2
+    pre = L.size_query("aima_moe_prefill_workspace_size", C.byref(lc), 2048, 8)
+    # act f16 [A+T][I] + contributions f32 [A+T][H] dominate
+    assert pre >= (16384 + 2048) * (512 * 2 + 2048 * 4)
+    stack = L.size_query("aima_moe_stack_prefill_workspace_size", C.byref(lc), 2048, 8)
+    assert stack >= pre + 3 * 2048 * 2048 * 2
+    sched = L.size_query("aima_grouped_schedule_workspace_size", 2048, 8, 256)
+    assert 0 < sched < pre
+
+
+def test_layer_validation(pkg):
+    L = pkg._lib
+    lib = L.lib()
+    p = C.c_void_p(1 << 20)
+    bad_group = _fake_layer(pkg, group=64)
+    rc = lib.aima_moe_grouped_prefill(C.byref(bad_group), p, None, 16, p, p, 8, p, p, 1 << 30,
+                                      None)
+    assert rc == L.AIMA_E_UNSUPPORTED
+    lc = _fake_layer(pkg)
+    rc = lib.aima_moe_grouped_prefill(C.byref(lc), p, None, 16, p, p, 8, p, p, 16, None)
+    assert rc == L.AIMA_E_WORKSPACE
+    rc = lib.aima_moe_ffn_decode(C.byref(lc), p, None, p, p, 300, p, p, 1 << 20, None)
+    assert rc == L.AIMA_E_INVALID  # k > experts
+    odd = _fake_layer(pkg, H=3000)
+    rc = lib.aima_moe_ffn_decode(C.byref(odd), p, None, p, p, 8, p, p, 1 << 30, None)
+    assert rc in (L.AIMA_E_INVALID, L.AIMA_E_UNSUPPORTED)
+    rc = lib.aima_moe_stack_decode(C.byref(lc), 0, 1e-6, p, p, p, 8, p, p, 1 << 30, None)
+    assert rc == L.AIMA_E_INVALID
+
+
+def test_python_layer_rejects_cpu_tensors(pkg):
+    layer = pkg.synth.moe_layer(hidden=256, inter=128, experts=8, seed=0, device="cpu")
+    x = torch.zeros(256, dtype=torch.float16)
+    ids = torch.zeros(8, dtype=torch.int32)
+    w = torch.zeros(8, dtype=torch.float32)
+    with pytest.raises(ValueError):
+        pkg.run_moe_ffn_layer(layer, x, ids, w)
+    with pytest.raises(ValueError):
+        pkg.matvec_u4(x, layer.shared_gate_up)
+
+
+def test_u4_weight_validation(pkg):
+    q = torch.zeros((4, 64), dtype=torch.uint8)
+    s = torch.zeros((4, 1), dtype=torch.float16)
+    z = torch.zeros(2, dtype=torch.uint8)
+    pkg.U4Weight(q, s, z, rows=4, k=128, group=128)
+    with pytest.raises(ValueError):
+        pkg.U4Weight(q, s, z, rows=4, k=256, group=128)
+    with pytest.raises(TypeError):
+        pkg.U4Weight(q, s.float(), z, rows=4, k=128, group=128)
+
+
+def test_synthetic_distributions(pkg):
+    layer = pkg.synth.moe_layer(hidden=256, inter=128, experts=4, seed=3, device="cpu")
+    s = layer.gate_up.scale.float()
+    assert float(s.min()) >= 1e-3 - 1e-6 and 0.01 < float(s.mean()) < 0.03
+    q = layer.gate_up.qweight
+    lo, hi = (q & 15).float().mean().item(), (q >> 4).float().mean().item()
+    assert 7.0 < lo < 8.0 and 7.0 < hi < 8.0
+    b = pkg.synth.zipf_bias(256, 1.1, seed=2, device="cpu")
+    p = torch.exp(b.double())
+    assert abs(float(p.sum()) - 1.0) < 1e-6  # f32 log-probabilities
+    assert float(p.max() / p.min()) > 400  # 256^1.1 ~ 446

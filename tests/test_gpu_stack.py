@@ -1,0 +1,142 @@
+"""GPU parity for the layer stacks (config 4): RMSNorm between layers, f16
+activations carried layer to layer.  Small stacks are checked on every token;
+the full 40-layer x 256-expert stack (~17 GB resident) is checked on the
+decode token and on sampled prefill tokens (tokens are independent through
+an MoE FFN stack, so a token subset is an exact check of those rows)."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests.helpers import assert_parity, f16_bits, f16_to_f32, moe_to_oracle, u4_to_oracle
+
+pytestmark = pytest.mark.gpu
+THREADS = min(16, os.cpu_count() or 1)
+EPS = 1e-6
+
+
+def oracle_stack(layers_np, norms, x_bits, ids, w):
+    """ids/w: [L][T][k] (already remapped to each layer's oracle experts)."""
+    r = x_bits
+    for L, mw in enumerate(layers_np):
+        rf = oracle.f16_values(r)
+        h = oracle.f16_values(oracle.float_to_half(oracle.rms_norm_rows(rf, norms[L], EPS))
+                              .reshape(rf.shape))
+        o = oracle.moe_ffn_tokens(mw, h, ids[L], w[L], residual=rf, threads=THREADS)
+        r = oracle.float_to_half(o).reshape(o.shape)
+    return r
+
+
+def compact_oracle_layer(layer, used):
+    """Oracle weights holding only the experts in `used` (in that order)."""
+    idx = torch.as_tensor(np.asarray(used, np.int64), device=layer.gate_up.qweight.device)
+
+    def pick(w):
+        sub = type(w)(w.qweight.index_select(0, idx).contiguous(),
+                      w.scale.index_select(0, idx).contiguous(),
+                      w.zp.index_select(0, idx).contiguous(), w.rows, w.k, w.group)
+        return u4_to_oracle(sub)
+
+    return oracle.MoeWeights(pick(layer.gate_up), pick(layer.down),
+                             u4_to_oracle(layer.shared_gate_up), u4_to_oracle(layer.shared_down),
+                             f16_bits(layer.shared_gate_vec))
+
+
+def remap(ids_np):
+    used, inv = np.unique(ids_np, return_inverse=True)
+    return used, inv.reshape(ids_np.shape).astype(np.int32)
+
+
+def make_stack(pkg, dev, n_layers, H, I, E, seed):
+    return [pkg.synth.moe_layer(hidden=H, inter=I, experts=E, seed=seed + l, device=dev)
+            for l in range(n_layers)]
+
+
+def routing(pkg, dev, n_layers, T, E, seed, k=8):
+    logits = torch.stack([pkg.synth.router_logits(T, E, seed + 1000 + l, dev)
+                          for l in range(n_layers)])
+    return pkg.select_router_topk(logits, k)
+
+
+def test_small_stack_decode_and_prefill(pkg, dev):
+    layers = make_stack(pkg, dev, 3, 512, 128, 16, seed=500)
+    lnp = [moe_to_oracle(l) for l in layers]
+    norms = [l.norm_weight.cpu().numpy() for l in layers]
+    # decode
+    x = pkg.synth.activations(1, 512, 1, dev)
+    ids, w = routing(pkg, dev, 3, 1, 16, 2)
+    out = pkg.moe_stack_decode(layers, x[0], ids[:, 0].contiguous(), w[:, 0].contiguous(),
+                               epsilon=EPS)
+    torch.cuda.synchronize()
+    ref = oracle_stack(lnp, norms, f16_bits(x), ids.cpu().numpy(), w.cpu().numpy())
+    assert_parity(f16_to_f32(out), oracle.f16_values(ref[0]), what="small stack decode")
+    # prefill
+    T = 97
+    x = pkg.synth.activations(T, 512, 3, dev)
+    ids, w = routing(pkg, dev, 3, T, 16, 4)
+    out = pkg.moe_stack_prefill(layers, x, ids, w, epsilon=EPS)
+    torch.cuda.synchronize()
+    ref = oracle_stack(lnp, norms, f16_bits(x), ids.cpu().numpy(), w.cpu().numpy())
+    assert_parity(f16_to_f32(out), oracle.f16_values(ref), what="small stack prefill")
+
+
+def test_stack_single_layer_equals_layer_ops(pkg, dev):
+    """One stack layer == RMSNorm, then the decode layer with the residual."""
+    layers = make_stack(pkg, dev, 1, 2048, 512, 32, seed=700)
+    x = pkg.synth.activations(1, 2048, 7, dev)[0]
+    ids, w = routing(pkg, dev, 1, 1, 32, 8)
+    a = pkg.moe_stack_decode(layers, x, ids[:, 0].contiguous(), w[:, 0].contiguous(), EPS)
+    h = pkg.apply_rms_norm(x[None], layers[0].norm_weight, EPS)[0]
+    b = pkg.run_moe_ffn_layer(layers[0], h, ids[0, 0].contiguous(), w[0, 0].contiguous(),
+                              residual=x)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+@pytest.fixture(scope="module")
+def stack40(pkg, dev):
+    layers = make_stack(pkg, dev, 40, 2048, 512, 256, seed=4000)
+    yield layers
+    del layers
+    torch.cuda.empty_cache()
+
+
+def _sampled_oracle(stack, x_bits, ids_np, w_np):
+    """Oracle through every layer using only the experts the sampled tokens use."""
+    r = x_bits
+    for L, layer in enumerate(stack):
+        used, rid = remap(ids_np[L])
+        mw = compact_oracle_layer(layer, used)
+        rf = oracle.f16_values(r)
+        h = oracle.f16_values(oracle.float_to_half(
+            oracle.rms_norm_rows(rf, layer.norm_weight.cpu().numpy(), EPS)).reshape(rf.shape))
+        o = oracle.moe_ffn_tokens(mw, h, rid, w_np[L], residual=rf, threads=THREADS)
+        r = oracle.float_to_half(o).reshape(o.shape)
+    return r
+
+
+def test_config4a_decode_40_layers(pkg, dev, stack40):
+    x = pkg.synth.activations(1, 2048, 41, dev)
+    ids, w = routing(pkg, dev, 40, 1, 256, 42)
+    out = pkg.moe_stack_decode(stack40, x[0], ids[:, 0].contiguous(), w[:, 0].contiguous(), EPS)
+    torch.cuda.synchronize()
+    ref = _sampled_oracle(stack40, f16_bits(x), ids.cpu().numpy(), w.cpu().numpy())
+    assert_parity(f16_to_f32(out), oracle.f16_values(ref[0]), what="config4a")
+
+
+def test_config4b_prefill_40_layers_sampled(pkg, dev, stack40):
+    T = 16384
+    x = pkg.synth.activations(T, 2048, 43, dev)
+    ids, w = routing(pkg, dev, 40, T, 256, 44)
+    out = pkg.moe_stack_prefill(stack40, x, ids, w, EPS)
+    torch.cuda.synchronize()
+    sel = np.array([0, 1, 5000, 16383])
+    ids_np = ids.cpu().numpy()[:, sel]
+    w_np = w.cpu().numpy()[:, sel]
+    ref = _sampled_oracle(stack40, f16_bits(x)[sel], ids_np, w_np)
+    got = f16_to_f32(out)[sel]
+    assert_parity(got, oracle.f16_values(ref), what="config4b sampled")
+    assert torch.isfinite(out.float()).all()
