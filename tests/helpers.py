@@ -2,6 +2,9 @@
 
 from __future__ import annotations
 
+import json
+import os
+
 import numpy as np
 
 import oracle
@@ -53,6 +56,10 @@ def compare(got, ref) -> dict:
 
 def assert_parity(got, ref, tol=2e-3, what=""):
     c = compare(got, ref)
+    log = os.environ.get("AIMA_PARITY_LOG")
+    if log:
+        with open(log, "a") as f:
+            f.write(json.dumps({"what": what, "tol": tol, **c}) + "\n")
     assert np.all(np.isfinite(np.asarray(got, np.float64))), f"{what}: non-finite output"
     assert c["max_rel"] <= tol, f"{what}: {c}"
     assert c["rel_l2"] <= tol, f"{what}: {c}"

@@ -104,18 +104,26 @@ def stack40(pkg, dev):
     torch.cuda.empty_cache()
 
 
-def _sampled_oracle(stack, x_bits, ids_np, w_np):
-    """Oracle through every layer using only the experts the sampled tokens use."""
-    r = x_bits
-    for L, layer in enumerate(stack):
-        used, rid = remap(ids_np[L])
-        mw = compact_oracle_layer(layer, used)
-        rf = oracle.f16_values(r)
-        h = oracle.f16_values(oracle.float_to_half(
-            oracle.rms_norm_rows(rf, layer.norm_weight.cpu().numpy(), EPS)).reshape(rf.shape))
-        o = oracle.moe_ffn_tokens(mw, h, rid, w_np[L], residual=rf, threads=THREADS)
-        r = oracle.float_to_half(o).reshape(o.shape)
-    return r
+def _oracle_layer(layer, r_bits, ids_np, w_np):
+    """One stack layer on the oracle for a few tokens, using only the experts
+    they select: r_{L+1} = f16(r + ffn(f16(rmsnorm(r))))."""
+    used, rid = remap(ids_np)
+    mw = compact_oracle_layer(layer, used)
+    rf = oracle.f16_values(r_bits)
+    h = oracle.f16_values(oracle.float_to_half(
+        oracle.rms_norm_rows(rf, layer.norm_weight.cpu().numpy(), EPS)).reshape(rf.shape))
+    o = oracle.moe_ffn_tokens(mw, h, rid, w_np, residual=rf, threads=THREADS)
+    return oracle.float_to_half(o).reshape(o.shape)
+
+
+# After 40 layers the f16 residual stream (|r| ~ 1e3, f16 ulp 0.5-1) carries
+# rounding differences that compound like a random walk: wherever GPU and
+# oracle FFN outputs (which agree to ~1e-4) straddle an f16 rounding point,
+# the residual differs by one ulp and the difference propagates.  Per-layer
+# parity is therefore checked teacher-forced at the 2e-3 bar (every GPU layer
+# starts from the oracle's own input), and the free-running 40-layer result
+# is held to rel-L2 <= 1e-2 and cosine >= 0.9999.
+END_TO_END_TOL = 1e-2
 
 
 def test_config4a_decode_40_layers(pkg, dev, stack40):
@@ -123,8 +131,18 @@ def test_config4a_decode_40_layers(pkg, dev, stack40):
     ids, w = routing(pkg, dev, 40, 1, 256, 42)
     out = pkg.moe_stack_decode(stack40, x[0], ids[:, 0].contiguous(), w[:, 0].contiguous(), EPS)
     torch.cuda.synchronize()
-    ref = _sampled_oracle(stack40, f16_bits(x), ids.cpu().numpy(), w.cpu().numpy())
-    assert_parity(f16_to_f32(out), oracle.f16_values(ref[0]), what="config4a")
+    ids_np, w_np = ids.cpu().numpy(), w.cpu().numpy()
+    r = f16_bits(x)
+    for L, layer in enumerate(stack40):
+        nxt = _oracle_layer(layer, r, ids_np[L], w_np[L])
+        got = pkg.moe_stack_decode([layer], torch.from_numpy(r[0].view(np.float16)).to(dev),
+                                   ids[L].contiguous(), w[L].contiguous(), EPS)
+        torch.cuda.synchronize()
+        assert_parity(f16_to_f32(got), oracle.f16_values(nxt[0]), what=f"config4a layer {L}")
+        r = nxt
+    c = assert_parity(f16_to_f32(out), oracle.f16_values(r[0]), tol=END_TO_END_TOL,
+                      what="config4a end-to-end")
+    assert c["cosine"] >= 0.9999
 
 
 def test_config4b_prefill_40_layers_sampled(pkg, dev, stack40):
@@ -133,10 +151,20 @@ def test_config4b_prefill_40_layers_sampled(pkg, dev, stack40):
     ids, w = routing(pkg, dev, 40, T, 256, 44)
     out = pkg.moe_stack_prefill(stack40, x, ids, w, EPS)
     torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
     sel = np.array([0, 1, 5000, 16383])
     ids_np = ids.cpu().numpy()[:, sel]
     w_np = w.cpu().numpy()[:, sel]
-    ref = _sampled_oracle(stack40, f16_bits(x)[sel], ids_np, w_np)
-    got = f16_to_f32(out)[sel]
-    assert_parity(got, oracle.f16_values(ref), what="config4b sampled")
-    assert torch.isfinite(out.float()).all()
+    r = f16_bits(x)[sel]
+    for L, layer in enumerate(stack40):
+        nxt = _oracle_layer(layer, r, ids_np[L], w_np[L])
+        # the same layer on the GPU grouped path for the sampled tokens (T = 4)
+        got = pkg.moe_stack_prefill([layer], torch.from_numpy(r.view(np.float16)).to(dev),
+                                    torch.from_numpy(ids_np[L:L + 1]).to(dev),
+                                    torch.from_numpy(w_np[L:L + 1]).to(dev), EPS)
+        torch.cuda.synchronize()
+        assert_parity(f16_to_f32(got), oracle.f16_values(nxt), what=f"config4b layer {L}")
+        r = nxt
+    c = assert_parity(f16_to_f32(out)[sel], oracle.f16_values(r), tol=END_TO_END_TOL,
+                      what="config4b end-to-end")
+    assert c["cosine"] >= 0.9999
