@@ -12,6 +12,7 @@ from ._lib import AimaError  # noqa: F401
 from .layout import MoeLayerWeights, U4Weight  # noqa: F401
 from .ops import (  # noqa: F401
     MIN_WEIGHT_SUM,
+    DecodePlan,
     Workspace,
     apply_rms_norm,
     build_grouped_schedule,

@@ -24,6 +24,7 @@ AIMA_E_WORKSPACE = -4
 AIMA_E_UNSUPPORTED = -5
 AIMA_DEVERR_EXPERT_RANGE = 1
 AIMA_DEVERR_EXPERT_DUPLICATE = 2
+AIMA_DEVERR_TIMEOUT = 4
 AIMA_OUT_F16 = 0
 AIMA_OUT_F32 = 1
 
@@ -72,6 +73,10 @@ SIGNATURES = {
     "aima_moe_stack_prefill": (C.c_int, [_LP, _i32, _f32, _vp, _i64, _vp, _vp, _i32, _vp, _vp,
                                          C.c_size_t, _vp]),
     "aima_workspace_error": (C.c_int, [_vp, C.POINTER(C.c_uint32), _vp]),
+    "aima_moe_decode_plan_create": (C.c_int, [_LP, _i32, _i32, C.POINTER(_vp)]),
+    "aima_moe_decode_plan_run": (C.c_int, [_vp, _f32, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),
+    "aima_moe_decode_plan_error": (C.c_int, [_vp, C.POINTER(C.c_uint32), _vp]),
+    "aima_moe_decode_plan_destroy": (C.c_int, [_vp]),
 }
 
 

@@ -49,6 +49,9 @@ inline size_t round_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 // Launch status check after a kernel launch.
 int launch_check(const char* what);
 
+// log2 of a supported group size (32, 64, 128, 256), else -1.
+int group_log2_of(int group);
+
 // ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------
@@ -71,12 +74,37 @@ __device__ __forceinline__ uint32_t u4_code(const uint8_t* packed, int64_t i) {
   return (i & 1) ? (b >> 4) : (b & 0x0fu);
 }
 
-// Wave64 butterfly sum over aligned segments of `width` lanes (power of two);
-// every lane of a segment ends with the segment total.
+// Sums over aligned lane segments with DPP (register-to-register lane moves,
+// a few cycles each, no LDS round trip).  Inside a 16-lane row:
+// quad_perm [1,0,3,2] and [2,3,0,1] give every lane its quad total,
+// row_half_mirror adds the mirrored quad of the 8-lane half, row_mirror the
+// mirrored half of the row, so every lane holds its row total.  Across rows
+// the four row totals are read with readlane (wave-uniform result).
+// Every lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+__device__ __forceinline__ float lane_read(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Every lane of each aligned WIDTH-lane segment ends with the segment total.
 template <int WIDTH>
 __device__ __forceinline__ float segment_sum(float v) {
-#pragma unroll
-  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  static_assert(WIDTH == 1 || WIDTH == 2 || WIDTH == 4 || WIDTH == 8 || WIDTH == 16 ||
+                    WIDTH == 32 || WIDTH == 64,
+                "segment width must be a power of two <= 64");
+  if (WIDTH >= 2) v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  if (WIDTH >= 4) v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  if (WIDTH >= 8) v += dpp_mov<0x141>(v);  // row_half_mirror
+  if (WIDTH >= 16) v += dpp_mov<0x140>(v); // row_mirror
+  if (WIDTH == 32) v += __shfl_xor(v, 16, 64);
+  if (WIDTH == 64) {
+    v = (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
+  }
   return v;
 }
 
@@ -141,6 +169,26 @@ __device__ __forceinline__ float u4_chunk_raw(const u32x4 w, const XChunk& c) {
 __device__ __forceinline__ float u4_chunk_dot(const u32x4 w, const XChunk& c,
                                               uint32_t z, float s) {
   return (u4_chunk_raw(w, c) - c.bias - (float)z * c.xsum) * s;
+}
+
+// Loads through pointers the compiler cannot prove global (e.g. read from a
+// device-side table) would otherwise become flat loads, which also count
+// against the LDS counter and so stall at the next LDS wait.  These force the
+// global address space.
+#define AIMA_GLOBAL __attribute__((address_space(1)))
+
+__device__ __forceinline__ u32x4 gload16_nt(const void* p) {
+  return __builtin_nontemporal_load((const AIMA_GLOBAL u32x4*)(p));
+}
+__device__ __forceinline__ float gload_h2f(const uint16_t* p, int64_t i) {
+  return h2f(((const AIMA_GLOBAL uint16_t*)(p))[i]);
+}
+__device__ __forceinline__ uint32_t gload_u4(const uint8_t* packed, int64_t i) {
+  const uint32_t b = ((const AIMA_GLOBAL uint8_t*)(packed))[i >> 1];
+  return (i & 1) ? (b >> 4) : (b & 0x0fu);
+}
+__device__ __forceinline__ u32x4 gload16(const void* p) {
+  return *((const AIMA_GLOBAL u32x4*)(p));
 }
 
 __device__ __forceinline__ u32x4 load16(const void* p) {

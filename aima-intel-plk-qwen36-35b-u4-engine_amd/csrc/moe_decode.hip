@@ -164,7 +164,8 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < G::NC; ++i) acc += u4_chunk_dot(w[ps][i], xc[i], z[ps][i], s[ps][i]);
-    v[ps] = ok[ps] ? segment_sum<G::SEG>(acc) : 0.f;
+    const float t = segment_sum<G::SEG>(acc);  // all lanes active here
+    v[ps] = ok[ps] ? t : 0.f;
   }
   // Gather the NR row sums: row ri lives in segment (ri % RPI) of pass ri / RPI.
   float rows[NR];

@@ -320,3 +320,76 @@ def moe_stack_prefill(layers: Sequence[MoeLayerWeights], x: torch.Tensor, ids: t
     call("aima_moe_stack_prefill", arr, L, float(epsilon), x.data_ptr(), T, ids.data_ptr(),
          weights.data_ptr(), k, out.data_ptr(), buf.data_ptr(), buf.numel(), _stream())
     return out
+
+
+class DecodePlan:
+    """Resident whole-stack decode: every layer of one token in one launch.
+
+    Mirrors the reference's resident native loop: ``DecodePlan(layers, k)``
+    uploads the layer table once; ``run`` executes RMSNorm -> MoE FFN ->
+    residual for every layer in a single cooperative kernel (graph-capturable,
+    no allocation).  Routing comes from ``router_logits`` [L, E] (the
+    select_router_topk rule) or from ``ids``/``weights`` [L, k].
+    Raises AimaError(AIMA_E_UNSUPPORTED) for shapes outside the specialization
+    (hidden 2048, inter 512, k <= 8); ``moe_stack_decode`` covers those.
+    """
+
+    def __init__(self, layers: Sequence[MoeLayerWeights], k: int = 8):
+        self.layers = list(layers)  # keep the weights alive
+        self.k = int(k)
+        self.hidden = self.layers[0].hidden
+        self._arr = _layers_c(self.layers)
+        h = C.c_void_p(0)
+        call("aima_moe_decode_plan_create", self._arr, len(self.layers), self.k, C.byref(h))
+        self._h = h
+
+    def run(self, residual: torch.Tensor, router_logits: Optional[torch.Tensor] = None,
+            ids: Optional[torch.Tensor] = None, weights: Optional[torch.Tensor] = None,
+            epsilon: float = 1e-6, min_weight_sum: float = MIN_WEIGHT_SUM,
+            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self._h is None:
+            raise RuntimeError("decode plan was closed")
+        _require_cuda(residual, router_logits, ids, weights)
+        L = len(self.layers)
+        if residual.dtype != torch.float16 or residual.numel() != self.hidden:
+            raise ValueError("residual must be float16 [hidden]")
+        if router_logits is not None:
+            if router_logits.dtype != torch.float32 or router_logits.dim() != 2 or \
+                    router_logits.shape[0] != L or not router_logits.is_contiguous():
+                raise ValueError("router_logits must be contiguous float32 [layers, experts]")
+            if router_logits.shape[1] != self.layers[0].experts:
+                raise ValueError("router_logits width must equal the expert count")
+        else:
+            if ids is None or weights is None:
+                raise ValueError("need router_logits or ids + weights")
+            if _check_route(ids, weights, L) != self.k:
+                raise ValueError("ids/weights must be [layers, k]")
+        if out is None:
+            out = torch.empty(self.hidden, dtype=torch.float16, device=residual.device)
+        call("aima_moe_decode_plan_run", self._h, float(epsilon), residual.data_ptr(),
+             _ptr(router_logits), _ptr(ids), _ptr(weights), float(min_weight_sum),
+             out.data_ptr(), _stream())
+        return out
+
+    def error_bits(self) -> int:
+        out = C.c_uint32(0)
+        call("aima_moe_decode_plan_error", self._h, C.byref(out), _stream())
+        return int(out.value)
+
+    def check(self) -> None:
+        bits = self.error_bits()
+        if bits & _lib.AIMA_DEVERR_TIMEOUT:
+            raise RuntimeError("persistent decode wait timed out")
+        if bits & _lib.AIMA_DEVERR_EXPERT_RANGE:
+            raise IndexError("expert id out of range")
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) is not None:
+            call("aima_moe_decode_plan_destroy", self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -47,6 +47,7 @@ extern "C" {
  * 2 = duplicated within a token; grouped_s8_u4_f16_contribution_moe.cl:38-53). */
 #define AIMA_DEVERR_EXPERT_RANGE 1u
 #define AIMA_DEVERR_EXPERT_DUPLICATE 2u
+#define AIMA_DEVERR_TIMEOUT 4u /* a persistent-kernel wait hit its spin limit */
 
 #define AIMA_OUT_F16 0
 #define AIMA_OUT_F32 1
@@ -217,6 +218,32 @@ int aima_moe_stack_decode(const aima_moe_layer* layers, int32_t n_layers,
                           const int32_t* ids, const float* weights, int32_t k,
                           uint16_t* out, void* workspace,
                           size_t workspace_bytes, void* stream);
+
+/* Resident decode plan: the whole n_layers-layer decode step in ONE
+ * cooperative launch (hidden 2048, inter 512, k <= 8; see
+ * moe_decode_persistent.hip).  create() validates the shapes, checks that
+ * the device keeps 256 blocks of 512 threads resident, allocates the plan's
+ * device buffers and uploads the layer table (synchronous, setup time only;
+ * AIMA_E_UNSUPPORTED when the shape or device does not fit, in which case
+ * aima_moe_stack_decode is the general path).  run() is asynchronous,
+ * allocates nothing and can be captured in a HIP graph: routing comes from
+ * router_logits [n_layers][experts] (the select_router_topk rule) or, when
+ * that is NULL, from ids/weights [n_layers][k]; out = r_{n_layers} as in
+ * aima_moe_stack_decode.  Calls on one plan must not overlap.  Mirrors the
+ * reference's resident native loop (engine/include/intel_qwen36/
+ * native_carrier_loop.hpp:38-100) for the MoE FFN stack. */
+typedef struct aima_moe_decode_plan aima_moe_decode_plan;
+int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t n_layers,
+                                int32_t k, aima_moe_decode_plan** plan);
+int aima_moe_decode_plan_run(aima_moe_decode_plan* plan, float eps,
+                             const uint16_t* residual_in,
+                             const float* router_logits, const int32_t* ids,
+                             const float* weights, float min_weight_sum,
+                             uint16_t* out, void* stream);
+/* Device error bits of the plan (AIMA_DEVERR_*; synchronizes, then clears). */
+int aima_moe_decode_plan_error(aima_moe_decode_plan* plan, uint32_t* error_bits,
+                               void* stream);
+int aima_moe_decode_plan_destroy(aima_moe_decode_plan* plan);
 
 /* Workspace bytes for aima_moe_stack_prefill (one layer's prefill workspace
  * plus the normalized activations). */

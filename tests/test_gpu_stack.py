@@ -168,3 +168,98 @@ def test_config4b_prefill_40_layers_sampled(pkg, dev, stack40):
     c = assert_parity(f16_to_f32(out)[sel], oracle.f16_values(r), tol=END_TO_END_TOL,
                       what="config4b end-to-end")
     assert c["cosine"] >= 0.9999
+
+
+# ---------------------------------------------------------------------------
+# resident persistent decode (one launch for all layers)
+# ---------------------------------------------------------------------------
+
+def test_decode_plan_small_stack(pkg, dev):
+    """3 layers of the real width (16 experts): persistent kernel vs oracle,
+    routing from logits and from explicit ids/weights; repeated runs (the
+    per-launch epochs must never match stale words of an earlier launch)."""
+    layers = make_stack(pkg, dev, 3, 2048, 512, 16, seed=900)
+    lnp = [moe_to_oracle(l) for l in layers]
+    norms = [l.norm_weight.cpu().numpy() for l in layers]
+    plan = pkg.DecodePlan(layers, k=8)
+    for rep in range(4):
+        x = pkg.synth.activations(1, 2048, 60 + rep, dev)
+        logits = torch.stack([pkg.synth.router_logits(1, 16, 70 + rep * 10 + l, dev)[0]
+                              for l in range(3)])
+        ids, w = pkg.select_router_topk(logits, 8)
+        a = plan.run(x[0], router_logits=logits)
+        b = plan.run(x[0], ids=ids, weights=w)
+        torch.cuda.synchronize()
+        assert plan.error_bits() == 0
+        assert torch.equal(a, b)
+        ref = oracle_stack(lnp, norms, f16_bits(x), ids.cpu().numpy()[:, None],
+                           w.cpu().numpy()[:, None])
+        assert_parity(f16_to_f32(a), oracle.f16_values(ref[0]), what=f"plan small rep={rep}")
+
+
+def test_decode_plan_flags_bad_ids(pkg, dev):
+    layers = make_stack(pkg, dev, 2, 2048, 512, 16, seed=950)
+    plan = pkg.DecodePlan(layers, k=8)
+    x = pkg.synth.activations(1, 2048, 1, dev)[0]
+    ids = torch.arange(8, dtype=torch.int32, device=dev).repeat(2, 1).contiguous()
+    ids[1, 3] = 40  # out of range for 16 experts
+    w = torch.full((2, 8), 0.125, device=dev)
+    out = plan.run(x, ids=ids, weights=w)
+    torch.cuda.synchronize()
+    bits = plan.error_bits()
+    assert bits & pkg._lib.AIMA_DEVERR_EXPERT_RANGE and not bits & pkg._lib.AIMA_DEVERR_TIMEOUT
+    assert torch.isfinite(out.float()).all()
+
+
+def test_decode_plan_graph_replays(pkg, dev):
+    """Captured once, replayed several times with eager work in between; every
+    replay equals the eager result."""
+    layers = make_stack(pkg, dev, 2, 2048, 512, 16, seed=960)
+    plan = pkg.DecodePlan(layers, k=8)
+    x = pkg.synth.activations(1, 2048, 5, dev)[0].contiguous()
+    logits = torch.stack([pkg.synth.router_logits(1, 16, 80 + l, dev)[0] for l in range(2)])
+    out = torch.empty(2048, dtype=torch.float16, device=dev)
+    eager = plan.run(x, router_logits=logits).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        plan.run(x, router_logits=logits, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        plan.run(x, router_logits=logits, out=out)
+    for _ in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        plan.run(x, router_logits=logits)  # eager work between replays
+        torch.cuda.synchronize()
+    assert plan.error_bits() == 0
+
+
+def test_config4a_decode_plan_40_layers(pkg, dev, stack40):
+    """The 40-layer persistent decode: every layer teacher-forced (1-layer
+    plans on the oracle's inputs) at the 2e-3 bar, plus the free-running
+    40-layer plan within the end-to-end bound."""
+    x = pkg.synth.activations(1, 2048, 141, dev)
+    logits = torch.stack([pkg.synth.router_logits(1, 256, 2141 + l, dev)[0] for l in range(40)])
+    ids, w = pkg.select_router_topk(logits, 8)
+    plan = pkg.DecodePlan(stack40, k=8)
+    out = plan.run(x[0], router_logits=logits)
+    torch.cuda.synchronize()
+    assert plan.error_bits() == 0
+    ids_np, w_np = ids.cpu().numpy(), w.cpu().numpy()
+    r = f16_bits(x)
+    for L, layer in enumerate(stack40):
+        nxt = _oracle_layer(layer, r, ids_np[L:L + 1], w_np[L:L + 1])
+        one = pkg.DecodePlan([layer], k=8)
+        got = one.run(torch.from_numpy(r[0].view(np.float16)).to(dev), ids=ids[L:L + 1],
+                      weights=w[L:L + 1])
+        torch.cuda.synchronize()
+        assert_parity(f16_to_f32(got), oracle.f16_values(nxt[0]), what=f"plan layer {L}")
+        one.close()
+        r = nxt
+    c = assert_parity(f16_to_f32(out), oracle.f16_values(r[0]), tol=END_TO_END_TOL,
+                      what="plan 40-layer end-to-end")
+    assert c["cosine"] >= 0.9999
