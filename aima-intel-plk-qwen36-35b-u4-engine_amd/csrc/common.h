@@ -55,8 +55,14 @@ int group_log2_of(int group);
 // ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------
+// Bit casts take their operand by value: __builtin_bit_cast applied directly
+// to an element of an ext_vector_type (v[i]) reads element 0 with this
+// compiler, so vector elements always pass through one of these helpers.
 __device__ __forceinline__ f16x2 as_h2(uint32_t v) {
   return __builtin_bit_cast(f16x2, v);
+}
+__device__ __forceinline__ float as_f32(uint32_t v) {
+  return __builtin_bit_cast(float, v);
 }
 __device__ __forceinline__ uint32_t h2_bits(f16x2 v) {
   return __builtin_bit_cast(uint32_t, v);
@@ -151,24 +157,34 @@ __device__ __forceinline__ void make_xchunk(const uint32_t (&xw)[16], XChunk& c)
   c.xsum = xe + xo;
 }
 
-__device__ __forceinline__ float u4_chunk_raw(const u32x4 w, const XChunk& c) {
+// 0x64006400 (two f16 1024.0) held in a VGPR.  With the nibble mask in an
+// SGPR, each "extract + bias" below is then a single v_and_or_b32 (a VOP3
+// instruction takes at most one scalar operand and no literal on gfx9).
+// Create it once outside a loop and pass it to the chunk routines.
+__device__ __forceinline__ uint32_t u4_magic() {
+  uint32_t m = 0x64006400u;
+  asm volatile("" : "+v"(m));
+  return m;
+}
+
+__device__ __forceinline__ float u4_chunk_raw(const u32x4 w, const XChunk& c, uint32_t magic) {
   float a1 = 0.f, a16 = 0.f;
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     const uint32_t v = w[d];
     const uint32_t v8 = v >> 8;
-    a1 = __builtin_amdgcn_fdot2(as_h2((v & 0x000F000Fu) | 0x64006400u), c.p[4 * d + 0], a1, false);
-    a16 = __builtin_amdgcn_fdot2(as_h2((v & 0x00F000F0u) | 0x64006400u), c.p[4 * d + 1], a16, false);
-    a1 = __builtin_amdgcn_fdot2(as_h2((v8 & 0x000F000Fu) | 0x64006400u), c.p[4 * d + 2], a1, false);
-    a16 = __builtin_amdgcn_fdot2(as_h2((v8 & 0x00F000F0u) | 0x64006400u), c.p[4 * d + 3], a16, false);
+    a1 = __builtin_amdgcn_fdot2(as_h2((v & 0x000F000Fu) | magic), c.p[4 * d + 0], a1, false);
+    a16 = __builtin_amdgcn_fdot2(as_h2((v & 0x00F000F0u) | magic), c.p[4 * d + 1], a16, false);
+    a1 = __builtin_amdgcn_fdot2(as_h2((v8 & 0x000F000Fu) | magic), c.p[4 * d + 2], a1, false);
+    a16 = __builtin_amdgcn_fdot2(as_h2((v8 & 0x00F000F0u) | magic), c.p[4 * d + 3], a16, false);
   }
   return a1 + a16 * 0.0625f;
 }
 
 // sum_k (q_k - z) * s * x_k over the chunk.
-__device__ __forceinline__ float u4_chunk_dot(const u32x4 w, const XChunk& c,
-                                              uint32_t z, float s) {
-  return (u4_chunk_raw(w, c) - c.bias - (float)z * c.xsum) * s;
+__device__ __forceinline__ float u4_chunk_dot(const u32x4 w, const XChunk& c, uint32_t z,
+                                              float s, uint32_t magic) {
+  return (u4_chunk_raw(w, c, magic) - c.bias - (float)z * c.xsum) * s;
 }
 
 // Loads through pointers the compiler cannot prove global (e.g. read from a

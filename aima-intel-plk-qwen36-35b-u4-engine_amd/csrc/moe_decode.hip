@@ -103,6 +103,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
   const int64_t groups = G::K / L.group;
   const int64_t total_pairs = (int64_t)(k + 1) * I;
   const int64_t pair0 = ((int64_t)blockIdx.x * 4 + wave) * kPairsPerWave;
+  const uint32_t magic = u4_magic();
 
   XChunk xc[G::NC];
   load_chunks<KCH>(x, cl, xc);
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
   for (int ps = 0; ps < PASSES; ++ps) {
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < G::NC; ++i) acc += u4_chunk_dot(w[ps][i], xc[i], z[ps][i], s[ps][i]);
+    for (int i = 0; i < G::NC; ++i) acc += u4_chunk_dot(w[ps][i], xc[i], z[ps][i], s[ps][i], magic);
     const float t = segment_sum<G::SEG>(acc);  // all lanes active here
     v[ps] = ok[ps] ? t : 0.f;
   }
@@ -216,6 +217,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(
   const int64_t I = L.inter;
   const int64_t groups = G::K / L.group;
   const int64_t h0 = (int64_t)blockIdx.x * kDownRowsPerBlock;
+  const uint32_t magic = u4_magic();
 
   float acc[PASSES];
 #pragma unroll
@@ -266,7 +268,7 @@ __global__ __launch_bounds__(256) void decode_down_kernel(
     for (int ps = 0; ps < PASSES; ++ps) {
       float d = 0.f;
 #pragma unroll
-      for (int i = 0; i < G::NC; ++i) d += u4_chunk_dot(w[ps][i], xc[i], z[ps][i], s[ps][i]);
+      for (int i = 0; i < G::NC; ++i) d += u4_chunk_dot(w[ps][i], xc[i], z[ps][i], s[ps][i], magic);
       acc[ps] += coef * d;
     }
   }

@@ -81,6 +81,7 @@ __global__ __launch_bounds__(256) void u4_matvec_kernel(
   const int seg = lane / G::SEG;
   const int cl = lane % G::SEG;
   const int64_t groups = (int64_t)G::K >> group_log2;
+  const uint32_t magic = u4_magic();
 
   XChunk xc[G::NC];
   load_x_chunks<KCH>(x, cl, xc);
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(256) void u4_matvec_kernel(
     const int64_t row = row0 + r * G::RPI + seg;
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < G::NC; ++i) acc += u4_chunk_dot(w[r][i], xc[i], z[r][i], s[r][i]);
+    for (int i = 0; i < G::NC; ++i) acc += u4_chunk_dot(w[r][i], xc[i], z[r][i], s[r][i], magic);
     acc = segment_sum<G::SEG>(acc);
     if (cl == 0 && row < n) {
       if (out_f32) {
