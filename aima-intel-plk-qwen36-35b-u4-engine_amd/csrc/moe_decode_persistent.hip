@@ -280,12 +280,12 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 #ifdef AIMA_DECODE_TRACE
 // Diagnostics build only (never in the product library): phase timestamps of
-// every block, 100 MHz real-time clock, g_trace[(L * 256 + block) * 8 + slot].
+// every block, 100 MHz real-time clock, g_trace[(L * 256 + block) * 16 + slot].
 __device__ uint64_t* g_trace = nullptr;
 #define AIMA_TRACE(L, slot, T)                                              \
   do {                                                                      \
     if (trace && threadIdx.x == (T) && b < 256)                             \
-      trace[((L) * 256 + b) * 8 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+      trace[((L) * 256 + b) * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
 #else
 #define AIMA_TRACE(L, slot, T) \
@@ -545,9 +545,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   AIMA_TRACE(40, 1, 0);  // prologue done
 
   // r_{L} polling: eight coalesced 16-byte device-coherent loads per lane
-  // (the volatile bit keeps the compiler from merging repeated polls); two
-  // batches stay in flight so a value is seen about half a round trip after
-  // it lands.
+  // (the volatile bit keeps the compiler from merging repeated polls), one
+  // batch at a time without pause: measured faster than keeping two batches
+  // in flight or sleeping between polls, which add fabric traffic or delay.
   constexpr int kAuxPoll = kAuxCoherent | (int)(1u << 31);
   auto issue_r = [&](const AIMA_GLOBAL uint8_t* src, uint32_t (&rv)[32]) {
     const int lane = opaque_v(threadIdx.x & 63);
@@ -565,8 +565,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     for (int q = 0; q < 32; ++q) ok = ok && (rv[q] >> 16) == ep;
     return __all(ok) != 0;
   };
-  // act_L polling: 24 records per lane, two batches in flight; each batch is
-  // staged into LDS as it is checked (a later complete batch overwrites it)
+  // act_L polling: 24 records per lane; each batch is staged into LDS as it
+  // is checked (a later complete batch overwrites it)
   constexpr int kQ = kActRecords / 64;
   const int nrec = (pairs + 2) / 3;  // valid records
   auto issue_act = [&](const uint64_t* src, uint64_t (&v)[kQ]) {
@@ -619,18 +619,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
         }
       } else {
         const AIMA_GLOBAL uint8_t* src = uptr(a.r_buf + ((L - 1) & 1) * kH);
-        uint32_t rw[32];
         uint32_t spins = 0;
-        issue_r(src, rv);
         while (true) {
-          issue_r(src, rw);
-          if (r_ready(rv, epR)) break;
           issue_r(src, rv);
-          if (r_ready(rw, epR)) {
-#pragma unroll
-            for (int q = 0; q < 32; ++q) rv[q] = rw[q];
-            break;
-          }
+          if (r_ready(rv, epR)) break;
           if (++spins > kSpinLimit) {
             fail_timeout();
             break;
@@ -731,7 +723,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
         st_coherent64(&a.act_buf[(L & 1) * kActRecords + pair0 / 3 + ct], rec);
       }
       AIMA_TRACE(L, 2, 64);
+      // Weight prefetches are issued where the compute waves would otherwise
+      // wait: a wave stalls at issue until the memory pipeline accepts its
+      // loads, which at the chip's streaming rate takes about a microsecond.
       prefetch_b(L);
+      AIMA_TRACE(L, 8, 64);
       if (L + 1 < a.n_layers) {
         load_vec(L + 1, vec);
         // the last compute wave fetches the next layer's route meanwhile
@@ -739,14 +735,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       }
     } else {
       const uint64_t* src = a.act_buf + (L & 1) * kActRecords;
-      uint64_t va[kQ], vb[kQ];
+      uint64_t va[kQ];
       uint32_t spins = 0;
-      issue_act(src, va);
       while (true) {
-        issue_act(src, vb);
-        if (stage_act(va, epA)) break;
         issue_act(src, va);
-        if (stage_act(vb, epA)) break;
+        if (stage_act(va, epA)) break;
         if (++spins > kSpinLimit) {
           fail_timeout();
           break;
@@ -755,6 +748,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       AIMA_TRACE(L, 3, 0);
     }
     __syncthreads();  // #3: act_L staged
+    AIMA_TRACE(L, 12, 64);
     if (S.abort) {
       finish();
       return;
@@ -771,6 +765,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
         }
       }
       wave_lds_sync();
+      AIMA_TRACE(L, 10, 64);
       const int seg = lane >> 4, cl = lane & 15;
 #pragma unroll
       for (int i = 0; i < kMaxUnitsB; ++i) {
@@ -786,12 +781,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
           if (cl == 0) S.part[slot][(u & 1) * 4 + seg] = d;
         }
       }
+      AIMA_TRACE(L, 11, 64);
       if (L + 1 < a.n_layers) store_vec(vec);
     }
     __syncthreads();  // #4: partial sums ready, next layer's vectors staged
     AIMA_TRACE(L, 4, 0);
     if (wave > 0) {
       if (L + 1 < a.n_layers) prefetch_a(L + 1);
+      AIMA_TRACE(L, 9, 64);
     } else if (lane < kRowsB) {
       // weighted sum in rank order, then the gated shared expert
       float c[kMaxK], pv[kMaxSlots];
