@@ -9,8 +9,13 @@ expert intermediate 512, group-128 U4, ~17 GB), one batch-1 decode step per
 MoE FFN -> residual through every layer.  ``value`` is us per decode token.
 
 The same line carries
-* ``roofline``: the dominant decode kernel (routed+shared gate/up + SwiGLU),
-  algorithmic bytes per launch / its event-timed average launch time;
+* ``roofline``: the dominant kernel, the persistent decode kernel (one launch
+  runs all 40 layers): algorithmic bytes per launch (the 8 routed + 1 shared
+  experts' U4 weights, scales and zero points of every layer, plus the
+  activations) / its event-timed average launch time on the launch stream;
+  ``traffic`` is the HBM bytes per launch measured with rocprofv3 PMC
+  counters (FETCH_SIZE + WRITE_SIZE, calibrated against a plain copy of
+  known size), read from the committed profile summary;
 * ``prefill``: grouped prefill of one layer at T=2048 (config 2, Zipf(1.1)
   skewed routing) in tok/s and MFMA fraction, and the 40-layer T=16384 chunk
   (config 4b);
@@ -138,6 +143,23 @@ def cpu_baseline(torch, pkg, oracle, layers, x, ids, w, budget_s=12.0):
             "host_cpu": _cpu_model()}
 
 
+def profiled_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed PMC summary
+    (profiles/*_pmc.md lines "traffic_bytes_per_launch <kernel> <bytes>"), or
+    None when no summary records it."""
+    d = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(d):
+        return None
+    for name in sorted(os.listdir(d)):
+        if not name.endswith("_pmc.md"):
+            continue
+        for line in open(os.path.join(d, name)):
+            parts = line.strip().strip("`").split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == kernel:
+                return int(parts[2])
+    return None
+
+
 def _cpu_model():
     try:
         for line in open("/proc/cpuinfo"):
@@ -156,6 +178,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="only the headline decode step (for profiling runs)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 1 GiB device copy 5 times (PMC counter "
+                         "calibration) and exit")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus > 1 or world > 1:
@@ -165,6 +190,17 @@ def main():
         sys.exit(2)
 
     import torch
+
+    if args.copy_calibration:
+        n = 1 << 30
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n, "copies": 5}), flush=True)
+        return
+
     import __graft_entry__
 
     pkg = __graft_entry__.load_package()
@@ -223,7 +259,8 @@ def main():
     per_launch_us = timed(torch, decode_step, args.steps, warmup=3)
     achieved = (weight_bytes + act_bytes) / per_launch_us / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": profiled_traffic("decode_persistent_kernel"),
                 "kernel": "decode_persistent_kernel", "bytes_per_launch": weight_bytes + act_bytes,
                 "avg_launch_us": round(per_launch_us, 3)}
     log(f"persistent decode kernel: {per_launch_us:.2f} us/launch, {achieved:.0f} GB/s")
