@@ -32,7 +32,6 @@ namespace aima {
 
 constexpr int kBM = 128;            // rows per M tile
 constexpr int kSchedBlock = 1024;   // assignments per schedule block
-constexpr int kLdsRowHalves = 136;  // 128 halves + 8 pad: 272-byte LDS rows
 constexpr int kMaxExperts = 1024;
 
 struct PrefillWs {
@@ -110,25 +109,60 @@ static size_t prefill_ws_layout(const PrefillDims& d, WsMode mode, void* base, P
 // covers the id range.  Eight-or-ten ballots replace a match-any.
 __device__ __forceinline__ uint64_t match_mask(int e, uint64_t active, int bits) {
   uint64_t m = active;
-  for (int b = 0; b < bits; ++b) {
-    const bool bit = (e >> b) & 1;
-    const uint64_t bal = __ballot(bit);
-    m &= bit ? bal : ~bal;
+#pragma unroll
+  for (int b = 0; b < 10; ++b) {  // ids < kMaxExperts = 2^10
+    if (b < bits) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t bal = __ballot(bit);
+      m &= bit ? bal : ~bal;
+    }
   }
   return m;
 }
 
-// Reads assignment a, validates it (range, duplicate within the token) and
-// returns the expert id clamped into range so that every later index stays
-// inside its buffer even for invalid input.
-__device__ __forceinline__ int sched_expert(const int32_t* __restrict__ ids, int64_t a, int k,
-                                            int E, uint32_t* err) {
-  const int e = ids[a];
+// The block's kSchedBlock ids, staged in LDS with coalesced 16-byte loads
+// (the per-assignment work below then never waits on global memory).
+__device__ __forceinline__ void stage_ids(const int32_t* __restrict__ ids, int64_t base, int64_t A,
+                                          int32_t* sid) {
+  const int lane = threadIdx.x;
+  if (base + kSchedBlock <= A && (reinterpret_cast<uintptr_t>(ids + base) & 15) == 0) {
+#pragma unroll
+    for (int i = 0; i < kSchedBlock / 256; ++i) {
+      const int q = lane + 64 * i;
+      reinterpret_cast<u32x4*>(sid)[q] = *reinterpret_cast<const u32x4*>(ids + base + 4 * q);
+    }
+  } else {
+    for (int i = lane; i < kSchedBlock; i += 64) sid[i] = base + i < A ? ids[base + i] : 0;
+  }
+  __syncthreads();
+}
+
+// Validates assignment a (range, duplicate within its token) from the staged
+// ids (earlier ids of a token that starts in the previous block are read from
+// global memory) and returns the expert id clamped into range, so every later
+// index stays inside its buffer even for invalid input.
+__device__ __forceinline__ int sched_expert(const int32_t* __restrict__ ids, const int32_t* sid,
+                                            int64_t base, int64_t a, int k, int E, uint32_t* err) {
+  const int e = sid[a - base];
   const int rank = (int)(a % k);
+  const int64_t t0 = a - rank;  // first assignment of the token
   uint32_t bad = 0;
   if (e < 0 || e >= E) bad |= AIMA_DEVERR_EXPERT_RANGE;
-  for (int p = 0; p < rank; ++p) {
-    if (ids[a - rank + p] == e) bad |= AIMA_DEVERR_EXPERT_DUPLICATE;
+  if (t0 >= base) {
+    // all earlier ids of the token are staged: independent, unconditional LDS
+    // reads (indices clamped into the block), compared only below `rank`
+    const int t0l = (int)(t0 - base);
+#pragma unroll
+    for (int p = 0; p < 15; ++p) {
+      const int o = sid[min(t0l + p, kSchedBlock - 1)];
+      if (p < rank && o == e) bad |= AIMA_DEVERR_EXPERT_DUPLICATE;
+    }
+  } else {
+    for (int p = 0; p < rank; ++p) {
+      const int64_t b = t0 + p;
+      const int o = b >= base ? sid[b - base] : ids[b];
+      if (o == e) bad |= AIMA_DEVERR_EXPERT_DUPLICATE;
+    }
   }
   if (bad) atomicOr(err, bad);
   return (e < 0 || e >= E) ? 0 : e;
@@ -139,14 +173,15 @@ __global__ __launch_bounds__(64) void sched_count_kernel(const int32_t* __restri
                                                          uint32_t* err,
                                                          int32_t* __restrict__ block_counts) {
   __shared__ int cnt[kMaxExperts];
+  __shared__ __attribute__((aligned(16))) int32_t sid[kSchedBlock];
   const int lane = threadIdx.x;
   for (int e = lane; e < E; e += 64) cnt[e] = 0;
-  __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSchedBlock;
+  stage_ids(ids, base, A, sid);
   for (int sub = 0; sub < kSchedBlock / 64; ++sub) {
     const int64_t a = base + sub * 64 + lane;
     const bool valid = a < A;
-    const int e = valid ? sched_expert(ids, a, k, E, err) : 0;
+    const int e = valid ? sched_expert(ids, sid, base, a, k, E, err) : 0;
     const uint64_t act = __ballot(valid);
     if (act == 0) break;
     const uint64_t m = match_mask(e, act, bits);
@@ -193,10 +228,16 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
   const int e = threadIdx.x;
   int total = 0;
   if (e < E) {
-    for (int64_t b = 0; b < nb; ++b) {
-      const int c = block_base[b * E + e];
-      block_base[b * E + e] = total;
-      total += c;
+    // eight independent loads in flight per step
+    for (int64_t b0 = 0; b0 < nb; b0 += 8) {
+      int c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = b0 + j < nb ? block_base[(b0 + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (b0 + j < nb) block_base[(b0 + j) * E + e] = total;
+        total += c[j];
+      }
     }
   }
   const int ntiles = (total + kBM - 1) / kBM;
@@ -204,7 +245,7 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
   const int begin = block_exclusive_scan_1024(total, smem, &all_rows);
   const int tbegin = block_exclusive_scan_1024(ntiles, smem, &all_tiles);
   if (e < E) {
-    for (int64_t b = 0; b < nb; ++b) block_base[b * E + e] += begin;
+    for (int64_t b = 0; b < nb; ++b) block_base[b * E + e] += begin;  // independent stores
     offsets[e] = begin + total;
     for (int t = 0; t < ntiles; ++t) {
       int32_t* td = tiles + 4 * (int64_t)(tbegin + t);
@@ -230,17 +271,26 @@ __global__ __launch_bounds__(64) void sched_scatter_kernel(
     int bits, const int32_t* __restrict__ block_base, int32_t* __restrict__ token_map,
     int32_t* __restrict__ inverse_map, float* __restrict__ row_weight) {
   __shared__ int cur[kMaxExperts];
+  __shared__ __attribute__((aligned(16))) int32_t sid[kSchedBlock];
   const int lane = threadIdx.x;
   for (int e = lane; e < E; e += 64) cur[e] = block_base[(int64_t)blockIdx.x * E + e];
-  __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSchedBlock;
+  stage_ids(ids, base, A, sid);
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  // the block's router weights, loaded up front (independent loads)
+  float wv[kSchedBlock / 64];
+#pragma unroll
+  for (int sub = 0; sub < kSchedBlock / 64; ++sub) {
+    const int64_t a = base + sub * 64 + lane;
+    wv[sub] = a < A ? weights[a] : 0.f;
+  }
+#pragma unroll
   for (int sub = 0; sub < kSchedBlock / 64; ++sub) {
     const int64_t a = base + sub * 64 + lane;
     const bool valid = a < A;
     int e = 0;
     if (valid) {
-      const int raw = ids[a];
+      const int raw = sid[a - base];
       e = (raw < 0 || raw >= E) ? 0 : raw;
     }
     const uint64_t act = __ballot(valid);
@@ -251,7 +301,7 @@ __global__ __launch_bounds__(64) void sched_scatter_kernel(
     if (valid) {
       token_map[pos] = (int32_t)(a / k);
       inverse_map[a] = pos;
-      row_weight[pos] = weights[a];
+      row_weight[pos] = wv[sub];
       if (lane == __ffsll((unsigned long long)m) - 1) cur[e] += __popcll(m);
     }
     __syncthreads();
@@ -261,34 +311,92 @@ __global__ __launch_bounds__(64) void sched_scatter_kernel(
 // ---------------------------------------------------------------------------
 // grouped GEMM
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ u32x4 permute_pairs(u32x4 v) {
-  // (x0,x1)(x2,x3)(x4,x5)(x6,x7) -> (x0,x4)(x1,x5)(x2,x6)(x3,x7)
-  return u32x4{__builtin_amdgcn_perm(v[2], v[0], 0x05040100u),
-               __builtin_amdgcn_perm(v[2], v[0], 0x07060302u),
-               __builtin_amdgcn_perm(v[3], v[1], 0x05040100u),
-               __builtin_amdgcn_perm(v[3], v[1], 0x07060302u)};
-}
-
-// 8 nibbles (k0..k7) -> exact f16 (q - z) in MFMA slot order k0,k4,k1,k5,k2,k6,k3,k7.
-__device__ __forceinline__ f16x8 dequant8(uint32_t d, uint32_t zz) {
-  const f16x2 zh = as_h2(zz);
-  const f16x2 p0 = as_h2((d & 0x000F000Fu) | 0x64006400u) - zh;
-  const f16x2 p1 = as_h2(((d >> 4) & 0x000F000Fu) | 0x64006400u) - zh;
-  const f16x2 p2 = as_h2(((d >> 8) & 0x000F000Fu) | 0x64006400u) - zh;
-  const f16x2 p3 = as_h2(((d >> 12) & 0x000F000Fu) | 0x64006400u) - zh;
+// 8 nibbles k0..k7 of one 32-bit word -> f16 (q - z) * s in natural order
+// (k0,k1),(k2,k3),(k4,k5),(k6,k7).  A byte permute copies byte i to bytes 0
+// and 2; masking 0x00F0000F leaves the even nibble as 1024 + q (low half) and
+// the odd one as 1024 + 16 q (high half), which use zz2 = {1024+z, 1024+16z}
+// and ss2 = {s, s/16}.  (q - z) is exact in f16 and (q - z) * s is rounded
+// once (relative error <= 2^-11), which keeps the group scale out of the f32
+// accumulators.  `magic` is 0x64006400 in a VGPR (one v_and_or_b32 per pair).
+__device__ __forceinline__ f16x8 dequant8(uint32_t d, f16x2 zz2, f16x2 ss2, uint32_t magic) {
+  const f16x2 p0 = (as_h2((__builtin_amdgcn_perm(d, d, 0x0C000C00u) & 0x00F0000Fu) | magic) - zz2) * ss2;
+  const f16x2 p1 = (as_h2((__builtin_amdgcn_perm(d, d, 0x0C010C01u) & 0x00F0000Fu) | magic) - zz2) * ss2;
+  const f16x2 p2 = (as_h2((__builtin_amdgcn_perm(d, d, 0x0C020C02u) & 0x00F0000Fu) | magic) - zz2) * ss2;
+  const f16x2 p3 = (as_h2((__builtin_amdgcn_perm(d, d, 0x0C030C03u) & 0x00F0000Fu) | magic) - zz2) * ss2;
   const u32x4 v{h2_bits(p0), h2_bits(p1), h2_bits(p2), h2_bits(p3)};
   return __builtin_bit_cast(f16x8, v);
 }
 
+// Direct global -> LDS loads (each lane's 16 or 4 bytes land at the
+// wave-uniform LDS address + lane * size), addressed as a wave-uniform base
+// (SGPRs) plus a 32-bit per-lane byte offset.  Issued through inline
+// assembly: the compiler then neither counts them nor orders LDS reads behind
+// them; the kernel waits for them itself (s_waitcnt vmcnt before its
+// barriers).  The s_nop gives the M0 write one wait state before its use.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* lds) {
+  return (uint32_t)reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) void*)lds);
+}
+// `lds` is the wave-uniform LDS byte address (see lds_addr).
+__device__ __forceinline__ void lds_load16(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds)
+               : "memory");
+}
+__device__ __forceinline__ void lds_load4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds)
+               : "memory");
+}
+
+// One block computes a 128-row M tile of one expert against 256 weight rows:
+// gate/up: 128 gate + 128 up rows (the same 128 intermediate columns), down:
+// 256 output columns.  8 waves; wave w owns all 128 M rows and one 32-column
+// block: (gate/up) gate rows j0 + 16 w .. +16 in MFMA columns 0..15 and the
+// matching up rows in columns 16..31, (down) rows 32 w .. +32.  So each
+// weight element is dequantized by exactly one lane of the block, and a lane
+// feeds 4 MFMAs (32x32x16, one per 32-row M block) with every dequantized
+// weight.  Two waves per SIMD.  The K loop runs over 128-wide quantization
+// groups.
+//
+// All operands of a group reach LDS by direct global->LDS loads (no register
+// staging), three groups in flight: the A tile (128 rows x 256 bytes,
+// gathered through the token map; piece p of row r sits in slot p ^ (r & 15)
+// so MFMA operand reads are free of bank conflicts), the packed weight bytes
+// of the 256 rows (16 KB, in the order the lanes consume them), and each
+// row's scale and zero-point words.
+//
+// Blocks are mapped XCD-aware: physical block p runs on XCD p % 8 (round-robin
+// dispatch), and each XCD walks a contiguous range of (M tile, N tile) pairs,
+// N tile fastest, so the N tiles of one M tile (same A rows) and consecutive M
+// tiles of one expert (same weight rows) share that XCD's L2.
+constexpr int kGemmThreads = 512;
+constexpr int kStageA = kBM * 256;        // bytes
+constexpr int kStageB = 256 * 64;         // bytes
+constexpr int kStageSZ = 2 * 256 * 4;     // bytes
+constexpr int kLoadsPerStage = 7;         // direct loads per wave per group
+
 template <bool GATEUP>
-__global__ __launch_bounds__(256, 1) void grouped_gemm_kernel(
+__global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
     aima_moe_layer L, const uint16_t* __restrict__ src, const int32_t* __restrict__ tiles,
     const int32_t* __restrict__ tile_count, const int32_t* __restrict__ token_map,
-    const float* __restrict__ row_weight, int64_t A, uint16_t* __restrict__ act_out,
-    float* __restrict__ contrib_out) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM * kLdsRowHalves];
-  const int tile = blockIdx.x;
-  if (tile >= *tile_count) return;
+    const float* __restrict__ row_weight, int64_t A, int ntiles_n,
+    uint16_t* __restrict__ act_out, float* __restrict__ contrib_out) {
+  // LDS: three stages of A tiles, weight bytes and scale / zero-point words,
+  // then the router weights of the tile's rows (down epilogue)
+  constexpr int kOffB = 3 * kStageA, kOffZ = kOffB + 3 * kStageB, kOffW = kOffZ + 3 * kStageSZ;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kOffW + kBM * 4];
+  const int total = *tile_count * ntiles_n;
+  const int per_xcd = (total + 7) / 8;
+  const int p = blockIdx.x;
+  const int logical = (p % 8) * per_xcd + p / 8;
+  if (p / 8 >= per_xcd || logical >= total) return;
+  const int tile = logical / ntiles_n;
+  const int ntile = logical - tile * ntiles_n;
+
   const int e = tiles[4 * tile + 0];
   const int64_t row0 = tiles[4 * tile + 1];
   const int rows = tiles[4 * tile + 2];
@@ -302,156 +410,173 @@ __global__ __launch_bounds__(256, 1) void grouped_gemm_kernel(
                                    : (e < E ? L.down : L.shared_down);
   const int64_t eoff = (e < E) ? e : 0;
   const uint8_t* qw = W.qweight + eoff * rows_e * (K / 2);
-  const uint16_t* sc = W.scale + eoff * rows_e * GK;
+  const uint8_t* sc = reinterpret_cast<const uint8_t*>(W.scale + eoff * rows_e * GK);
   const uint8_t* zp = W.zp + eoff * (rows_e * GK / 2);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, hh = lane >> 5;
 
-  // B rows owned by this lane (one per N block).
-  int64_t wr[2];
-  if (GATEUP) {
-    const int64_t jb = (int64_t)blockIdx.y * 128 + wave * 32;
-    wr[0] = jb + n;
-    wr[1] = I + jb + n;
-  } else {
-    const int64_t hb = (int64_t)blockIdx.y * 256 + wave * 64;
-    wr[0] = hb + n;
-    wr[1] = hb + 32 + n;
-  }
+  // weight row of MFMA column n_ of column block w_
+  auto wrow = [&](int w_, int n_) -> int64_t {
+    if (GATEUP) {
+      const int64_t j = (int64_t)ntile * 128 + w_ * 16 + (n_ & 15);
+      return n_ < 16 ? j : I + j;
+    }
+    return (int64_t)ntile * 256 + w_ * 32 + n_;
+  };
+  const int64_t my_row = wrow(wave, n);
 
-  // A rows loaded by this thread: rr_i = (tid >> 4) + 16 i, part = tid & 15.
-  const int part = tid & 15;
-  const uint16_t* arow[8];
+  // --- direct-load sources of this lane: uniform bases + 32-bit offsets ---
+  // A: block instruction q = 4 wave + i covers rows 4q .. 4q+3; lane -> row
+  // 4q + lane/16, LDS slot lane%16 holding piece (lane%16) ^ (row & 15).
+  // Rows past the tile read the tile's first row (valid memory; their
+  // results are never stored).  (Byte offsets stay below 2^31: the host
+  // limits tokens * hidden.)
+  const void* a_base = uniform_ptr(src);
+  uint32_t aoff[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int rr = (tid >> 4) + 16 * i;
-    if (rr < rows) {
-      const int64_t grow = row0 + rr;
-      int64_t srow;
-      if (GATEUP) {
-        srow = (e < E) ? (int64_t)token_map[grow] : grow - A;
-      } else {
-        srow = grow;
-      }
-      arow[i] = src + srow * K + part * 8;
+  for (int i = 0; i < 4; ++i) {
+    const int r = 4 * (4 * wave + i) + (lane >> 4);
+    const int64_t grow = row0 + (r < rows ? r : 0);
+    int64_t srow;
+    if (GATEUP) {
+      srow = (e < E) ? (int64_t)token_map[grow] : grow - A;
     } else {
-      arow[i] = nullptr;
+      srow = grow;
     }
+    const int piece = (lane & 15) ^ (r & 15);
+    aoff[i] = (uint32_t)((srow * K + piece * 8) * 2);
   }
-
-  u32x4 areg[8];
-  auto load_a = [&](int g) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      areg[i] = arow[i] ? load16(arow[i] + g * 128) : u32x4{0u, 0u, 0u, 0u};
-    }
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int rr = (tid >> 4) + 16 * i;
-      *reinterpret_cast<u32x4*>(&As[buf][rr * kLdsRowHalves + part * 8]) = permute_pairs(areg[i]);
-    }
-  };
-  u32x4 braw[2][2];
-  float bs[2];
-  uint32_t bzz[2];
-  auto load_b = [&](int g, u32x4 (&raw)[2][2], float (&s)[2], uint32_t (&zz)[2]) {
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const uint8_t* p = qw + wr[nb] * (K / 2) + g * 64 + hh * 32;
-      raw[nb][0] = load16_nt(p);
-      raw[nb][1] = load16_nt(p + 16);
-      const int64_t gi = wr[nb] * GK + g;
-      s[nb] = h2f(sc[gi]);
-      zz[nb] = (0x6400u | u4_code(zp, gi)) * 0x00010001u;
-    }
-  };
-
-  const int mb_active = (rows + 31) / 32;
-  f32x16 acc[4][2];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = f32x16{};
+  // B: wave w loads its own column block: 16-byte piece t of the 32 bytes
+  // lane (n, hh) consumes (k 64 hh .. +64 of the group)
+  const void* b_base = uniform_ptr(qw);
+  const uint32_t boff = (uint32_t)(my_row * (K / 2) + hh * 32);
+  // scale / zero-point words: wave w loads word set w: scales for w < 4,
+  // zero points for w >= 4; lane -> word (w % 4) * 64 + lane of column block
+  // idx / 32, column idx % 32
+  int64_t sz_row;
+  {
+    const int idx = (wave & 3) * 64 + lane;
+    sz_row = wrow(idx >> 5, idx & 31);
   }
+  const bool sz_is_zero = wave >= 4;
+  const void* z_base = uniform_ptr(sz_is_zero ? zp : sc);
 
-  load_a(0);
-  load_b(0, braw, bs, bzz);
-  store_a(0);
-  __syncthreads();
+  // LDS destinations: the LDS base address plus wave-uniform integer offsets
+  const uint32_t lds0 = lds_addr(smem);
+  auto issue = [&](int g, int st) {
+    const uint32_t la = lds0 + (uint32_t)(st * kStageA + wave * 4096);
+    const uint32_t lb = lds0 + (uint32_t)(kOffB + st * kStageB + wave * 2048);
+    const uint32_t lz = lds0 + (uint32_t)(kOffZ + st * kStageSZ + wave * 256);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) lds_load16(a_base, aoff[i] + g * 256, la + i * 1024);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) lds_load16(b_base, boff + g * 64 + t * 16, lb + t * 1024);
+    const int64_t gi = sz_row * GK + g;
+    const uint32_t zoff = sz_is_zero ? (uint32_t)((gi >> 1) & ~(int64_t)3)
+                                     : (uint32_t)((gi * 2) & ~(int64_t)3);
+    lds_load4(z_base, zoff, lz);
+  };
 
-  for (int g = 0; g < GK; ++g) {
-    const int buf = g & 1;
-    u32x4 nraw[2][2];
-    float ns[2];
-    uint32_t nzz[2];
-    const bool more = g + 1 < GK;
-    if (more) {
-      load_a(g + 1);
-      load_b(g + 1, nraw, ns, nzz);
+  // M blocks that hold rows of the tile
+  const int mb_active = min(4, (rows + 31) / 32);
+  f32x16 acc[4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x16{};
+  const uint32_t magic = u4_magic();
+
+  auto compute = [&](int g, int st) {
+    const uint8_t* sA = smem + st * kStageA;
+    const uint8_t* sB = smem + kOffB + st * kStageB;
+    const uint32_t* sZ = reinterpret_cast<const uint32_t*>(smem + kOffZ + st * kStageSZ);
+    const int col = wave * 32 + n;  // word index within a set
+    const uint32_t sw = sZ[col];
+    const uint32_t zw = sZ[256 + col];
+    const int64_t gi = my_row * GK + g;
+    const uint32_t sbits = (sw >> ((gi & 1) * 16)) & 0xffffu;
+    const uint32_t z = (zw >> ((gi & 7) * 4)) & 0xfu;
+    const f16x2 s2 = as_h2(sbits * 0x00010001u);
+    const f16x2 ss2 = f16x2{s2.x, (_Float16)(s2.y * (_Float16)0.0625f)};
+    const f16x2 zz2 = as_h2((0x6400u | z) | ((0x6400u | (z << 4)) << 16));
+    u32x4 braw[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      braw[t] = *reinterpret_cast<const u32x4*>(sB + ((2 * wave + t) * 64 + lane) * 16);
     }
-    f32x16 accg[4][2];
-    const uint16_t* abase = &As[buf][n * kLdsRowHalves + hh * 64];
+    auto afrag = [&](int mb, int j) {
+      const int m = mb * 32 + n;
+      const int slot = (hh * 8 + j) ^ (m & 15);
+      return *reinterpret_cast<const f16x8*>(sA + m * 256 + slot * 16);
+    };
+    // All four M blocks run unconditionally (rows past the tile hold valid
+    // copies of row 0 and are never stored): straight-line code in which the
+    // A fragments of k-step j+1 load and its weights dequantize while the
+    // MFMAs of step j run.
+    f16x8 af[2][4];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) af[0][mb] = afrag(mb, 0);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      f16x8 b[2];
+      if (j + 1 < 8) {
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) b[nb] = dequant8(braw[nb][j >> 2][j & 3], bzz[nb]);
+        for (int mb = 0; mb < 4; ++mb) af[(j + 1) & 1][mb] = afrag(mb, j + 1);
+      }
+      const f16x8 b = dequant8(braw[j >> 2][j & 3], zz2, ss2, magic);
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
-        if (mb < mb_active) {
-          const f16x8 a = *reinterpret_cast<const f16x8*>(abase + mb * 32 * kLdsRowHalves + j * 8);
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) {
-            accg[mb][nb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                a, b[nb], j == 0 ? f32x16{} : accg[mb][nb], 0, 0, 0);
-          }
-        }
+        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][mb], b, acc[mb], 0, 0, 0);
       }
     }
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
-      if (mb < mb_active) {
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-          for (int v = 0; v < 16; ++v) acc[mb][nb][v] += bs[nb] * accg[mb][nb][v];
-        }
-      }
+  };
+
+  // Pipeline: groups g+1 and g+2 load while g computes.  Before computing g
+  // a wave waits for its own loads of g (those of g+1, issued later, may stay
+  // in flight), then the barrier makes every wave's loads of g visible and
+  // guarantees every wave is done with the stage that g+2 reuses.  The
+  // barrier is a plain s_barrier between compiler memory barriers: no fence,
+  // so it does not wait for the loads in flight.
+  auto sync_stage = [&](bool last) {
+    if (!last) {
+      asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    if (more) {
-      store_a(buf ^ 1);
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        braw[nb][0] = nraw[nb][0];
-        braw[nb][1] = nraw[nb][1];
-        bs[nb] = ns[nb];
-        bzz[nb] = nzz[nb];
-      }
-    }
-    __syncthreads();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  static_assert(kLoadsPerStage == 7, "the vmcnt(7) above counts one stage's loads");
+  issue(0, 0);
+  if (GK > 1) issue(1, 1);
+  for (int g = 0, st = 0; g < GK; ++g, st = (st == 2 ? 0 : st + 1)) {
+    sync_stage(g + 1 >= GK);
+    if (g + 2 < GK) issue(g + 2, st == 0 ? 2 : st - 1);
+    compute(g, st);
   }
 
   // Epilogue.  32x32 MFMA output: lane holds column n, rows
-  // 8*(v/4) + 4*hh + (v%4) of its M block.
+  // 8*(v/4) + 4*hh + (v%4) of its M block.  (down: the rows' router weights
+  // are staged in LDS first, one load per row)
+  float* s_wt = reinterpret_cast<float*>(smem + kOffW);
+  if (!GATEUP) {
+    if (tid < kBM) s_wt[tid] = (e < E && tid < rows) ? row_weight[row0 + tid] : 1.0f;
+    __syncthreads();
+  }
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb) {
     if (mb < mb_active) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = mb * 32 + 8 * (v >> 2) + 4 * hh + (v & 3);
-        if (r < rows) {
-          const int64_t grow = row0 + r;
-          if (GATEUP) {
-            act_out[grow * I + (wr[0])] = f2h(silu_mul(acc[mb][0][v], acc[mb][1][v]));
-          } else {
-            const float wt = (e < E) ? row_weight[grow] : 1.0f;
-            contrib_out[grow * H + wr[0]] = wt * acc[mb][0][v];
-            contrib_out[grow * H + wr[1]] = wt * acc[mb][1][v];
+        if (GATEUP) {
+          // gate in columns 0..15, up in 16..31 of the same lane half
+          const float other = __shfl_xor(acc[mb][v], 16, 64);
+          if (n < 16 && r < rows) {
+            act_out[(row0 + r) * I + my_row] = f2h(silu_mul(acc[mb][v], other));
           }
+        } else if (r < rows) {
+          contrib_out[(row0 + r) * H + my_row] = s_wt[r] * acc[mb][v];
         }
       }
     }
@@ -527,19 +652,33 @@ static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint1
                          const PrefillDims& d, const PrefillWs& w, hipStream_t st) {
   int rc = launch_schedule(ids, weights, d, w, st);
   if (rc != AIMA_OK) return rc;
-  hipLaunchKernelGGL((grouped_gemm_kernel<true>), dim3((unsigned)d.max_tiles, d.I / 128), dim3(256),
-                     0, st, L, x, w.tiles, w.tile_count, w.token_map, w.row_weight, d.A, w.act,
-                     w.contrib);
+  {
+    const int nt = d.I / 128;
+    const unsigned grid = (unsigned)round_up(d.max_tiles * nt, 8);
+    hipLaunchKernelGGL((grouped_gemm_kernel<true>), dim3(grid), dim3(kGemmThreads), 0, st, L, x,
+                       w.tiles, w.tile_count, w.token_map, w.row_weight, d.A, nt, w.act,
+                       w.contrib);
+  }
   rc = launch_check("grouped gate/up GEMM");
   if (rc != AIMA_OK) return rc;
-  hipLaunchKernelGGL((grouped_gemm_kernel<false>), dim3((unsigned)d.max_tiles, d.H / 256),
-                     dim3(256), 0, st, L, w.act, w.tiles, w.tile_count, w.token_map,
-                     w.row_weight, d.A, w.act, w.contrib);
+  {
+    const int nt = d.H / 256;
+    const unsigned grid = (unsigned)round_up(d.max_tiles * nt, 8);
+    hipLaunchKernelGGL((grouped_gemm_kernel<false>), dim3(grid), dim3(kGemmThreads), 0, st, L,
+                       w.act, w.tiles, w.tile_count, w.token_map, w.row_weight, d.A, nt, w.act,
+                       w.contrib);
+  }
   rc = launch_check("grouped down GEMM");
   if (rc != AIMA_OK) return rc;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)d.T), dim3(256), 0, st, w.contrib,
                      w.inverse_map, d.k, d.A, x, L.shared_gate_vec, residual, (int64_t)d.H, out);
   return launch_check("grouped combine");
+}
+
+// The grouped GEMM addresses its A rows with 32-bit byte offsets.
+static bool prefill_offsets_fit(const aima_moe_layer* L, int64_t tokens, int k) {
+  const int64_t limit = (int64_t)1 << 30;  // f16 elements (2^31 bytes)
+  return tokens * (k + 1) * L->inter < limit && tokens * L->hidden < limit;
 }
 
 int check_layer_prefill(const aima_moe_layer* L, int k, bool need_norm) {
@@ -597,6 +736,9 @@ extern "C" int aima_moe_grouped_prefill(const aima_moe_layer* layer, const uint1
   if (rc != AIMA_OK) return rc;
   AIMA_REQUIRE(x && ids && weights && out, "moe_grouped_prefill: null pointer");
   AIMA_REQUIRE(tokens > 0 && tokens <= (1 << 24), "moe_grouped_prefill: tokens must be in [1, 2^24]");
+  AIMA_REQUIRE(prefill_offsets_fit(layer, tokens, k),
+               "moe_grouped_prefill: tokens * (k + 1) * inter and tokens * hidden must stay below "
+               "2^30 (split the batch)");
   AIMA_REQUIRE(aligned(x, 16), "moe_grouped_prefill: x must be 16-byte aligned");
   const PrefillDims d = prefill_dims(layer, tokens, k);
   PrefillWs w{};
@@ -615,6 +757,9 @@ extern "C" int aima_moe_stack_prefill(const aima_moe_layer* layers, int32_t n_la
   AIMA_REQUIRE(layers && n_layers > 0, "moe_stack_prefill: need at least one layer");
   AIMA_REQUIRE(x_in && ids && weights && out, "moe_stack_prefill: null pointer");
   AIMA_REQUIRE(tokens > 0 && tokens <= (1 << 24), "moe_stack_prefill: tokens must be in [1, 2^24]");
+  AIMA_REQUIRE(prefill_offsets_fit(layers, tokens, k),
+               "moe_stack_prefill: tokens * (k + 1) * inter and tokens * hidden must stay below "
+               "2^30 (split the batch)");
   for (int32_t l = 0; l < n_layers; ++l) {
     int rc = check_layer_prefill(&layers[l], k, true);
     if (rc != AIMA_OK) return rc;

