@@ -1,27 +1,28 @@
 // Grouped MoE prefill on gfx950.
 //
-// 1. Device schedule (three small launches): a stable counting sort of the
-//    T*k (token, rank) assignments by expert.  Rows of one expert are ordered
-//    by assignment index, the order of the reference's host
-//    BuildGroupedSchedule (grouped_s8_u4_prefill_runtime.cpp:231-346), so the
-//    schedule is deterministic and bit-comparable with the CPU restatement.
-//    The scan also emits the list of 128-row M tiles (routed experts, then the
-//    shared expert over all T tokens).
+// 1. Device schedule (three launches): a stable counting sort of the T*k
+//    (token, rank) assignments by expert.  Rows of one expert are ordered by
+//    assignment index, the order of the reference's host BuildGroupedSchedule
+//    (grouped_s8_u4_prefill_runtime.cpp:231-346), so the schedule is
+//    deterministic and bit-comparable with the CPU restatement.  The scan
+//    also emits the M tiles (up to 256 rows of one expert; the shared expert
+//    covers all T tokens), ordered by height, tallest first.
 // 2. Grouped gate/up GEMM (MFMA v_mfma_f32_32x32x16_f16): per tile, the token
-//    rows are gathered into LDS (double-buffered per 128-wide K group); each
-//    wave dequantizes its own 64 weight rows (32 gate + the matching 32 up)
-//    straight from HBM into MFMA B operands as exact f16 (q - z), runs 8
-//    K-steps into a per-group accumulator and folds it into the f32 total
-//    with the group's f16 scale.  The SwiGLU epilogue writes f16 [rows][I].
-// 3. Grouped down GEMM, same structure over K = I, epilogue multiplies by the
-//    router weight and writes f32 contributions [rows][H].
+//    rows are gathered into LDS; each wave dequantizes its own 32 weight rows
+//    straight into MFMA operands as f16 (q - z) * s and multiplies them with
+//    every token row of the tile.  The SwiGLU epilogue writes f16 [rows][I].
+// 3. Grouped down GEMM, same structure over K = I; the epilogue multiplies by
+//    the router weight and writes f16 contributions [rows][H].
 // 4. Combine: per token, the k contributions in rank order, plus the
-//    sigmoid-gated shared row, plus the residual, rounded to f16.
+//    sigmoid-gated shared row, plus the residual, summed in f32 and rounded
+//    to f16.
 //
 // f16 rather than bf16 operands: the activations arrive as f16 and (q - z) is
-// an integer in [-15, 15], so every MFMA product is exact and the only
-// rounding besides f32 accumulation is the f16 SwiGLU output; MI355X runs
-// dense f16 and bf16 MFMA at the same rate.
+// an integer in [-15, 15], so (q - z) * s is the only operand rounding (once,
+// relative error <= 2^-11) besides the f16 SwiGLU output and the f16
+// contributions (the reference's GPU path also keeps f16 contributions,
+// grouped_s8_u4_f16_contribution_moe.cl:831-845); MI355X runs dense f16 and
+// bf16 MFMA at the same rate.
 #include "common.h"
 
 #include <math.h>
@@ -30,21 +31,22 @@
 
 namespace aima {
 
-constexpr int kBM = 128;            // rows per M tile
-constexpr int kSchedBlock = 1024;   // assignments per schedule block
+constexpr int kBM = 256;            // rows per M tile (8 MFMA blocks of 32)
+constexpr int kSchedBlock = 256;    // assignments per schedule block
 constexpr int kMaxExperts = 1024;
+constexpr int kTileClasses = 8;     // tile heights 32, 64, ..., 256 rows
 
 struct PrefillWs {
   uint32_t* err;
   int32_t* tile_count;
-  int32_t* block_base;   // [nb][E]
+  int32_t* block_base;   // [nb][E] block counts, then global row bases
   int32_t* offsets;      // [E] exclusive end of each expert's rows
   int32_t* tiles;        // [max_tiles][4]: expert, row0, rows, 0
   int32_t* token_map;    // [A]
-  int32_t* inverse_map;  // [A]
+  int32_t* inverse_map;  // [A] (local ranks between count and scatter)
   float* row_weight;     // [A]
-  uint16_t* act;         // [A + T][I]
-  float* contrib;        // [A + T][H]
+  uint16_t* act;         // [A + T][I] f16
+  uint16_t* contrib;     // [A + T][H] f16
   uint16_t* h;           // [T][H]   (stack only)
   uint16_t* r[2];        // [T][H]   (stack only)
 };
@@ -63,6 +65,7 @@ static PrefillDims prefill_dims(const aima_moe_layer* L, int64_t T, int k) {
   d.H = L->hidden;
   d.I = L->inter;
   d.nb = (d.A + kSchedBlock - 1) / kSchedBlock;
+  // every expert with rows adds at most one partial tile
   d.max_tiles = (d.A + kBM - 1) / kBM + std::min<int64_t>(d.E, d.A) + (T + kBM - 1) / kBM;
   return d;
 }
@@ -90,7 +93,7 @@ static size_t prefill_ws_layout(const PrefillDims& d, WsMode mode, void* base, P
   l.row_weight = reinterpret_cast<float*>(take((size_t)d.A * 4));
   if (mode != WsMode::kSchedule) {
     l.act = reinterpret_cast<uint16_t*>(take((size_t)(d.A + d.T) * d.I * 2));
-    l.contrib = reinterpret_cast<float*>(take((size_t)(d.A + d.T) * d.H * 4));
+    l.contrib = reinterpret_cast<uint16_t*>(take((size_t)(d.A + d.T) * d.H * 2));
   }
   if (mode == WsMode::kStack) {
     l.h = reinterpret_cast<uint16_t*>(take((size_t)d.T * d.H * 2));
@@ -106,7 +109,7 @@ static size_t prefill_ws_layout(const PrefillDims& d, WsMode mode, void* base, P
 // ---------------------------------------------------------------------------
 
 // Mask of the lanes (among `active`) holding the same expert id; `bits`
-// covers the id range.  Eight-or-ten ballots replace a match-any.
+// covers the id range.  Up to ten ballots replace a match-any.
 __device__ __forceinline__ uint64_t match_mask(int e, uint64_t active, int bits) {
   uint64_t m = active;
 #pragma unroll
@@ -120,75 +123,58 @@ __device__ __forceinline__ uint64_t match_mask(int e, uint64_t active, int bits)
   return m;
 }
 
-// The block's kSchedBlock ids, staged in LDS with coalesced 16-byte loads
-// (the per-assignment work below then never waits on global memory).
-__device__ __forceinline__ void stage_ids(const int32_t* __restrict__ ids, int64_t base, int64_t A,
-                                          int32_t* sid) {
-  const int lane = threadIdx.x;
-  if (base + kSchedBlock <= A && (reinterpret_cast<uintptr_t>(ids + base) & 15) == 0) {
-#pragma unroll
-    for (int i = 0; i < kSchedBlock / 256; ++i) {
-      const int q = lane + 64 * i;
-      reinterpret_cast<u32x4*>(sid)[q] = *reinterpret_cast<const u32x4*>(ids + base + 4 * q);
-    }
-  } else {
-    for (int i = lane; i < kSchedBlock; i += 64) sid[i] = base + i < A ? ids[base + i] : 0;
+// One thread per assignment.  Validates the id (range, duplicate among the
+// earlier ranks of its token), ranks it among the block's assignments of the
+// same expert in assignment order (ballot match inside each wave plus the
+// counts of the earlier waves), and writes the block's per-expert counts.
+// The local rank is parked in inverse_map until the scatter.
+__global__ __launch_bounds__(kSchedBlock) void sched_count_kernel(
+    const int32_t* __restrict__ ids, int32_t A, int k, int E, int bits, uint32_t* err,
+    int32_t* __restrict__ block_counts, int32_t* __restrict__ local_rank) {
+  __shared__ int cnt[kSchedBlock / 64][kMaxExperts];
+  __shared__ int32_t sid[16 + kSchedBlock];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int32_t base = (int32_t)blockIdx.x * kSchedBlock;
+  for (int w = 0; w < kSchedBlock / 64; ++w) {
+    for (int e = tid; e < E; e += kSchedBlock) cnt[w][e] = 0;
+  }
+  // the block's ids and the 16 before them (earlier ranks of a token that
+  // starts in the previous block)
+  for (int i = tid; i < 16 + kSchedBlock; i += kSchedBlock) {
+    const int32_t a = base - 16 + i;
+    sid[i] = (a >= 0 && a < A) ? ids[a] : -1;
   }
   __syncthreads();
-}
-
-// Validates assignment a (range, duplicate within its token) from the staged
-// ids (earlier ids of a token that starts in the previous block are read from
-// global memory) and returns the expert id clamped into range, so every later
-// index stays inside its buffer even for invalid input.
-__device__ __forceinline__ int sched_expert(const int32_t* __restrict__ ids, const int32_t* sid,
-                                            int64_t base, int64_t a, int k, int E, uint32_t* err) {
-  const int e = sid[a - base];
-  const int rank = (int)(a % k);
-  const int64_t t0 = a - rank;  // first assignment of the token
-  uint32_t bad = 0;
-  if (e < 0 || e >= E) bad |= AIMA_DEVERR_EXPERT_RANGE;
-  if (t0 >= base) {
-    // all earlier ids of the token are staged: independent, unconditional LDS
-    // reads (indices clamped into the block), compared only below `rank`
-    const int t0l = (int)(t0 - base);
+  const int32_t a = base + tid;
+  const bool valid = a < A;
+  int e = 0;
+  if (valid) {
+    const int raw = sid[16 + tid];
+    const int rank = a % k;
+    uint32_t bad = (raw < 0 || raw >= E) ? AIMA_DEVERR_EXPERT_RANGE : 0u;
 #pragma unroll
-    for (int p = 0; p < 15; ++p) {
-      const int o = sid[min(t0l + p, kSchedBlock - 1)];
-      if (p < rank && o == e) bad |= AIMA_DEVERR_EXPERT_DUPLICATE;
+    for (int p = 1; p < 16; ++p) {
+      if (p <= rank && sid[16 + tid - p] == raw) bad |= AIMA_DEVERR_EXPERT_DUPLICATE;
     }
-  } else {
-    for (int p = 0; p < rank; ++p) {
-      const int64_t b = t0 + p;
-      const int o = b >= base ? sid[b - base] : ids[b];
-      if (o == e) bad |= AIMA_DEVERR_EXPERT_DUPLICATE;
-    }
+    if (bad) atomicOr(err, bad);
+    e = (raw < 0 || raw >= E) ? 0 : raw;
   }
-  if (bad) atomicOr(err, bad);
-  return (e < 0 || e >= E) ? 0 : e;
-}
-
-__global__ __launch_bounds__(64) void sched_count_kernel(const int32_t* __restrict__ ids,
-                                                         int64_t A, int k, int E, int bits,
-                                                         uint32_t* err,
-                                                         int32_t* __restrict__ block_counts) {
-  __shared__ int cnt[kMaxExperts];
-  __shared__ __attribute__((aligned(16))) int32_t sid[kSchedBlock];
-  const int lane = threadIdx.x;
-  for (int e = lane; e < E; e += 64) cnt[e] = 0;
-  const int64_t base = (int64_t)blockIdx.x * kSchedBlock;
-  stage_ids(ids, base, A, sid);
-  for (int sub = 0; sub < kSchedBlock / 64; ++sub) {
-    const int64_t a = base + sub * 64 + lane;
-    const bool valid = a < A;
-    const int e = valid ? sched_expert(ids, sid, base, a, k, E, err) : 0;
-    const uint64_t act = __ballot(valid);
-    if (act == 0) break;
-    const uint64_t m = match_mask(e, act, bits);
-    if (valid && lane == __ffsll((unsigned long long)m) - 1) cnt[e] += __popcll(m);
-    __syncthreads();
+  const uint64_t m = match_mask(e, __ballot(valid), bits);
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  const int wrank = __popcll(m & below);
+  if (valid && wrank == 0) cnt[wave][e] = __popcll(m);
+  __syncthreads();
+  if (valid) {
+    int r = wrank;
+    for (int w = 0; w < wave; ++w) r += cnt[w][e];
+    local_rank[a] = r;
   }
-  for (int e = lane; e < E; e += 64) block_counts[(int64_t)blockIdx.x * E + e] = cnt[e];
+  for (int x = tid; x < E; x += kSchedBlock) {
+    int s = 0;
+#pragma unroll
+    for (int w = 0; w < kSchedBlock / 64; ++w) s += cnt[w][x];
+    block_counts[(int64_t)blockIdx.x * E + x] = s;
+  }
 }
 
 // Exclusive scan over the 1024 threads of a block; returns the prefix and
@@ -219,93 +205,122 @@ __device__ int block_exclusive_scan_1024(int v, int* smem, int* total) {
   return r;
 }
 
-__global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ block_base,
-                                                          int64_t nb, int E, int64_t T,
-                                                          int64_t A, int32_t* __restrict__ offsets,
-                                                          int32_t* __restrict__ tiles,
-                                                          int32_t* __restrict__ tile_count) {
-  __shared__ int smem[32];
-  const int e = threadIdx.x;
-  int total = 0;
-  if (e < E) {
-    // eight independent loads in flight per step
-    for (int64_t b0 = 0; b0 < nb; b0 += 8) {
-      int c[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) c[j] = b0 + j < nb ? block_base[(b0 + j) * E + e] : 0;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (b0 + j < nb) block_base[(b0 + j) * E + e] = total;
-        total += c[j];
-      }
-    }
-  }
-  const int ntiles = (total + kBM - 1) / kBM;
-  int all_rows, all_tiles;
-  const int begin = block_exclusive_scan_1024(total, smem, &all_rows);
-  const int tbegin = block_exclusive_scan_1024(ntiles, smem, &all_tiles);
-  if (e < E) {
-    for (int64_t b = 0; b < nb; ++b) block_base[b * E + e] += begin;  // independent stores
-    offsets[e] = begin + total;
-    for (int t = 0; t < ntiles; ++t) {
-      int32_t* td = tiles + 4 * (int64_t)(tbegin + t);
+// Tiles of one expert with `total` rows in class c (1..8 MFMA blocks of 32
+// rows): full 256-row tiles are class 8, the remainder tile is class
+// ceil(rem / 32).
+__device__ __forceinline__ int tiles_in_class(int total, int c) {
+  const int rem = total % kBM;
+  const int cls = (rem + 31) / 32;
+  return (c == kTileClasses ? total / kBM : 0) + (cls == c ? 1 : 0);
+}
+
+// Writes the class-c tiles of one expert starting at tile index `at`.
+__device__ __forceinline__ void write_tiles(int32_t* __restrict__ tiles, int at, int c, int e,
+                                            int begin, int total) {
+  const int full = total / kBM, rem = total % kBM;
+  const int cls = (rem + 31) / 32;
+  int t = at;
+  if (c == kTileClasses) {
+    for (int i = 0; i < full; ++i, ++t) {
+      int32_t* td = tiles + 4 * (int64_t)t;
       td[0] = e;
-      td[1] = begin + t * kBM;
-      td[2] = min(kBM, total - t * kBM);
+      td[1] = begin + i * kBM;
+      td[2] = kBM;
       td[3] = 0;
     }
   }
-  const int64_t shared_tiles = (T + kBM - 1) / kBM;
-  for (int64_t t = e; t < shared_tiles; t += 1024) {
-    int32_t* td = tiles + 4 * (all_tiles + t);
-    td[0] = E;
-    td[1] = (int)(A + t * kBM);
-    td[2] = (int)min((int64_t)kBM, T - t * kBM);
+  if (cls == c) {
+    int32_t* td = tiles + 4 * (int64_t)t;
+    td[0] = e;
+    td[1] = begin + full * kBM;
+    td[2] = rem;
     td[3] = 0;
   }
-  if (e == 0) *tile_count = all_tiles + (int)shared_tiles;
 }
 
-__global__ __launch_bounds__(64) void sched_scatter_kernel(
-    const int32_t* __restrict__ ids, const float* __restrict__ weights, int64_t A, int k, int E,
-    int bits, const int32_t* __restrict__ block_base, int32_t* __restrict__ token_map,
+// One block of 1024 threads: thread (p, e) with e = tid % Ep (Ep = E rounded
+// up to a power of two) scans chunk p of expert e's block counts, the chunk
+// partial sums are combined through LDS, and the experts' totals are scanned
+// into row offsets and into tile positions per class (class 8 first).
+__global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ block_base,
+                                                          int32_t nb, int E, int Ep, int32_t T,
+                                                          int32_t A, int32_t* __restrict__ offsets,
+                                                          int32_t* __restrict__ tiles,
+                                                          int32_t* __restrict__ tile_count) {
+  __shared__ int smem[32];
+  __shared__ int part[1024];
+  const int tid = threadIdx.x;
+  const int e = tid % Ep, pidx = tid / Ep, P = 1024 / Ep;
+  const int chunk = (nb + P - 1) / P;
+  const int b0 = pidx * chunk, b1 = min(nb, b0 + chunk);
+  int sum = 0;
+  if (e < E) {
+    for (int b = b0; b < b1; b += 8) {
+      int c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = b + j < b1 ? block_base[(int64_t)(b + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sum += c[j];
+    }
+  }
+  part[tid] = sum;
+  __syncthreads();
+  int before = 0, total = 0;
+  for (int q = 0; q < P; ++q) {
+    const int v = part[q * Ep + e];
+    if (q < pidx) before += v;
+    total += v;
+  }
+  const bool rep = pidx == 0 && e < E;
+  int all_rows;
+  const int begin = block_exclusive_scan_1024(rep ? total : 0, smem, &all_rows);
+  if (rep) offsets[e] = begin + total;
+  // expert e's row base reaches every chunk thread through LDS
+  __syncthreads();
+  if (pidx == 0) part[e] = begin;
+  __syncthreads();
+  if (e < E) {
+    int run = part[e] + before;
+    for (int b = b0; b < b1; b += 8) {
+      int c[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) c[j] = b + j < b1 ? block_base[(int64_t)(b + j) * E + e] : 0;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (b + j < b1) block_base[(int64_t)(b + j) * E + e] = run;
+        run += c[j];
+      }
+    }
+  }
+  // tiles, by class (tallest first); the shared expert's tiles follow the
+  // routed ones of each class
+  int cbase = 0;
+  for (int c = kTileClasses; c >= 1; --c) {
+    int routed;
+    const int n = rep ? tiles_in_class(total, c) : 0;
+    const int at = block_exclusive_scan_1024(n, smem, &routed);
+    if (rep && n) write_tiles(tiles, cbase + at, c, e, begin, total);
+    const int ns = tiles_in_class(T, c);
+    if (tid == 0 && ns) write_tiles(tiles, cbase + routed, c, E, A, T);
+    cbase += routed + ns;
+  }
+  if (tid == 0) *tile_count = cbase;
+}
+
+// One thread per assignment: the row = block base of its expert + its local
+// rank.
+__global__ __launch_bounds__(kSchedBlock) void sched_scatter_kernel(
+    const int32_t* __restrict__ ids, const float* __restrict__ weights, int32_t A, int k, int E,
+    const int32_t* __restrict__ block_base, int32_t* __restrict__ token_map,
     int32_t* __restrict__ inverse_map, float* __restrict__ row_weight) {
-  __shared__ int cur[kMaxExperts];
-  __shared__ __attribute__((aligned(16))) int32_t sid[kSchedBlock];
-  const int lane = threadIdx.x;
-  for (int e = lane; e < E; e += 64) cur[e] = block_base[(int64_t)blockIdx.x * E + e];
-  const int64_t base = (int64_t)blockIdx.x * kSchedBlock;
-  stage_ids(ids, base, A, sid);
-  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  // the block's router weights, loaded up front (independent loads)
-  float wv[kSchedBlock / 64];
-#pragma unroll
-  for (int sub = 0; sub < kSchedBlock / 64; ++sub) {
-    const int64_t a = base + sub * 64 + lane;
-    wv[sub] = a < A ? weights[a] : 0.f;
-  }
-#pragma unroll
-  for (int sub = 0; sub < kSchedBlock / 64; ++sub) {
-    const int64_t a = base + sub * 64 + lane;
-    const bool valid = a < A;
-    int e = 0;
-    if (valid) {
-      const int raw = sid[a - base];
-      e = (raw < 0 || raw >= E) ? 0 : raw;
-    }
-    const uint64_t act = __ballot(valid);
-    if (act == 0) break;
-    const uint64_t m = match_mask(e, act, bits);
-    const int pos = cur[e] + __popcll(m & below);
-    __syncthreads();
-    if (valid) {
-      token_map[pos] = (int32_t)(a / k);
-      inverse_map[a] = pos;
-      row_weight[pos] = wv[sub];
-      if (lane == __ffsll((unsigned long long)m) - 1) cur[e] += __popcll(m);
-    }
-    __syncthreads();
-  }
+  const int32_t a = (int32_t)blockIdx.x * kSchedBlock + threadIdx.x;
+  if (a >= A) return;
+  const int raw = ids[a];
+  const int e = (raw < 0 || raw >= E) ? 0 : raw;
+  const int pos = block_base[(int64_t)blockIdx.x * E + e] + inverse_map[a];
+  token_map[pos] = a / k;
+  inverse_map[a] = pos;
+  row_weight[pos] = weights[a];
 }
 
 // ---------------------------------------------------------------------------
@@ -351,235 +366,272 @@ __device__ __forceinline__ void lds_load4(const void* base, uint32_t off, uint32
   asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds)
                : "memory");
 }
+// Waits until at most N of this wave's vector memory operations are pending.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 6, "vmcnt immediate");
+  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  if constexpr (N == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+  if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+}
+// Block barrier that does not wait for outstanding memory operations (the
+// waves wait for their own loads first).
+__device__ __forceinline__ void plain_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
-// One block computes a 128-row M tile of one expert against 256 weight rows:
-// gate/up: 128 gate + 128 up rows (the same 128 intermediate columns), down:
-// 256 output columns.  8 waves; wave w owns all 128 M rows and one 32-column
-// block: (gate/up) gate rows j0 + 16 w .. +16 in MFMA columns 0..15 and the
-// matching up rows in columns 16..31, (down) rows 32 w .. +32.  So each
-// weight element is dequantized by exactly one lane of the block, and a lane
-// feeds 4 MFMAs (32x32x16, one per 32-row M block) with every dequantized
-// weight.  Two waves per SIMD.  The K loop runs over 128-wide quantization
-// groups.
+// One block computes an M tile (up to 256 token rows of one expert) against
+// 256 weight rows: gate/up: 128 gate + 128 up rows (the same 128
+// intermediate columns), down: 256 output columns.  8 waves; wave w owns 32
+// weight rows and every token row of the tile.  The weights are the MFMA A
+// operand (lane l dequantizes weight row l % 32, 8 k values per k-step) and
+// the token rows the B operand (MFMA block mb = token rows 32 mb .. +32), so
+// each dequantized weight feeds MB MFMAs, and the 32x32 result leaves lane
+// (n, hh) with 4 consecutive weight rows 8 q + 4 hh .. +3 (q = 0..3) of token
+// row n: the epilogue stores 8-byte runs of output columns.  For gate/up the
+// 32 weight rows of a wave are arranged so that q = 0, 1 are gate rows and
+// q = 2, 3 the up rows of the same 16 columns; SwiGLU needs no lane exchange.
 //
-// All operands of a group reach LDS by direct global->LDS loads (no register
-// staging), three groups in flight: the A tile (128 rows x 256 bytes,
-// gathered through the token map; piece p of row r sits in slot p ^ (r & 15)
-// so MFMA operand reads are free of bank conflicts), the packed weight bytes
-// of the 256 rows (16 KB, in the order the lanes consume them), and each
-// row's scale and zero-point words.
+// The K loop runs in stages of 64 (half a quantization group).  All operands
+// of a stage reach LDS by direct global->LDS loads, three stages in flight:
+// the token rows (256 rows x 128 bytes, gathered through the token map;
+// 16-byte piece p of row r sits in slot p ^ ((r >> 1) & 7), which keeps MFMA
+// operand reads free of bank conflicts), each wave's packed weight bytes
+// (32 rows x 32 bytes, in lane order) and the rows' scale and zero-point
+// words.  MB (1..8) is the tile height in 32-row blocks: rows past the tile
+// are neither loaded (beyond the MB blocks) nor multiplied.
 //
-// Blocks are mapped XCD-aware: physical block p runs on XCD p % 8 (round-robin
-// dispatch), and each XCD walks a contiguous range of (M tile, N tile) pairs,
-// N tile fastest, so the N tiles of one M tile (same A rows) and consecutive M
-// tiles of one expert (same weight rows) share that XCD's L2.
+// Blocks are mapped XCD-aware: physical block p runs on XCD p % 8
+// (round-robin dispatch); M tile i goes to XCD i % 8 and the N tiles of one M
+// tile (same token rows) are consecutive on that XCD, so they share its L2.
+// Tiles come tallest first, so each XCD works through large tiles first.
 constexpr int kGemmThreads = 512;
-constexpr int kStageA = kBM * 256;        // bytes
-constexpr int kStageB = 256 * 64;         // bytes
-constexpr int kStageSZ = 2 * 256 * 4;     // bytes
-constexpr int kLoadsPerStage = 7;         // direct loads per wave per group
+constexpr int kStageK = 64;                   // K per pipeline stage
+constexpr int kStageA = kBM * kStageK * 2;    // token rows, bytes
+constexpr int kStageB = 256 * kStageK / 2;    // packed weights, bytes
+constexpr int kStageSZ = 2 * 256 * 4;         // scale and zero-point words
+constexpr int kOffB = 3 * kStageA;
+constexpr int kOffZ = kOffB + 3 * kStageB;
+constexpr int kSmemBytes = kOffZ + 3 * kStageSZ;
+
+struct GemmTile {
+  const void* a_base;   // token rows (uniform)
+  const void* b_base;   // packed weights of the expert (uniform)
+  const void* z_base;   // scale or zero-point words (uniform)
+  uint32_t aoff[4];     // per-lane byte offsets of the token-row pieces
+  uint32_t boff;        // per-lane byte offset of the weight bytes
+  int64_t sz_row;       // weight row whose scale / zero word this lane loads
+  int64_t my_row;       // weight row this lane dequantizes
+  int GK, S;            // quantization groups, stages
+  int e, E, rows;
+  int64_t row0;
+  int ntile;
+  bool sz_is_zero;
+};
+
+template <bool GATEUP, int MB>
+__device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
+                                          const aima_moe_layer& L,
+                                          const float* __restrict__ row_weight,
+                                          uint16_t* __restrict__ act_out,
+                                          uint16_t* __restrict__ contrib_out) {
+  constexpr int NA = (MB + 1) / 2;   // token-row loads per wave per stage
+  constexpr int NL = NA + 2;         // + weight bytes + scale / zero word
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 31, hh = lane >> 5;
+  const uint32_t lds0 = lds_addr(smem);
+
+  auto issue = [&](int s, int st) {
+    const uint32_t la = lds0 + (uint32_t)(st * kStageA + wave * 1024);
+#pragma unroll
+    for (int i = 0; i < NA; ++i) lds_load16(t.a_base, t.aoff[i] + s * 128, la + i * 8192);
+    lds_load16(t.b_base, t.boff + s * 32, lds0 + (uint32_t)(kOffB + st * kStageB + wave * 1024));
+    const int64_t gi = t.sz_row * t.GK + (s >> 1);
+    const uint32_t zoff = t.sz_is_zero ? (uint32_t)((gi >> 1) & ~(int64_t)3)
+                                       : (uint32_t)((gi * 2) & ~(int64_t)3);
+    lds_load4(t.z_base, zoff, lds0 + (uint32_t)(kOffZ + st * kStageSZ + wave * 256));
+  };
+
+  f32x16 acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
+  const uint32_t magic = u4_magic();
+  const int swz = (n >> 1) & 7;  // token row m = 32 mb + n: (m >> 1) & 7
+
+  auto compute = [&](int s, int st) {
+    const uint8_t* sA = smem + st * kStageA;
+    const uint32_t* sZ = reinterpret_cast<const uint32_t*>(smem + kOffZ + st * kStageSZ);
+    const int col = wave * 32 + n;
+    const uint32_t sw = sZ[col];
+    const uint32_t zw = sZ[256 + col];
+    const int64_t gi = t.my_row * t.GK + (s >> 1);
+    const uint32_t sbits = (sw >> ((gi & 1) * 16)) & 0xffffu;
+    const uint32_t z = (zw >> ((gi & 7) * 4)) & 0xfu;
+    const f16x2 s2 = as_h2(sbits * 0x00010001u);
+    const f16x2 ss2 = f16x2{s2.x, (_Float16)(s2.y * (_Float16)0.0625f)};
+    const f16x2 zz2 = as_h2((0x6400u | z) | ((0x6400u | (z << 4)) << 16));
+    const u32x4 braw =
+        *reinterpret_cast<const u32x4*>(smem + kOffB + st * kStageB + wave * 1024 + lane * 16);
+    auto bfrag = [&](int mb, int j) {
+      const int slot = (hh * 4 + j) ^ swz;
+      return *reinterpret_cast<const f16x8*>(sA + (mb * 32 + n) * 128 + slot * 16);
+    };
+    f16x8 bf[2][MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) bf[0][mb] = bfrag(mb, 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (j + 1 < 4) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) bf[(j + 1) & 1][mb] = bfrag(mb, j + 1);
+      }
+      const f16x8 a = dequant8(braw[j], zz2, ss2, magic);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bf[j & 1][mb], acc[mb], 0, 0, 0);
+      }
+    }
+  };
+
+  // Pipeline: stages s+1 and s+2 load while s computes.  Before computing s a
+  // wave waits for its own loads of s (those of s+1, issued later, may stay
+  // in flight), then the barrier makes every wave's loads of s visible and
+  // guarantees every wave is done with the buffer that s+2 reuses.
+  const int S = t.S;
+  issue(0, 0);
+  issue(1, 1);
+  for (int s = 0, st = 0; s < S; ++s, st = (st == 2 ? 0 : st + 1)) {
+    if (s + 1 < S) {
+      wait_vmcnt<NL>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    plain_barrier();
+    if (s + 2 < S) issue(s + 2, st == 0 ? 2 : st - 1);
+    compute(s, st);
+  }
+
+  // Epilogue: lane (n, hh) of MFMA block mb holds token row m = 32 mb + n and
+  // weight rows 8 q + 4 hh + c in acc[mb][4 q + c].
+  const int64_t H = L.hidden, I = L.inter;
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = mb * 32 + n;
+    if (m < t.rows) {
+      const int64_t row = t.row0 + m;
+      if (GATEUP) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          u32x2 v;
+          v.x = (uint32_t)f2h(silu_mul(acc[mb][4 * q + 0], acc[mb][8 + 4 * q + 0])) |
+                ((uint32_t)f2h(silu_mul(acc[mb][4 * q + 1], acc[mb][8 + 4 * q + 1])) << 16);
+          v.y = (uint32_t)f2h(silu_mul(acc[mb][4 * q + 2], acc[mb][8 + 4 * q + 2])) |
+                ((uint32_t)f2h(silu_mul(acc[mb][4 * q + 3], acc[mb][8 + 4 * q + 3])) << 16);
+          const int64_t c0 = (int64_t)t.ntile * 128 + wave * 16 + 8 * q + 4 * hh;
+          *reinterpret_cast<u32x2*>(act_out + row * I + c0) = v;
+        }
+      } else {
+        const float wt = t.e < t.E ? row_weight[row] : 1.0f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          u32x2 v;
+          v.x = (uint32_t)f2h(wt * acc[mb][4 * q + 0]) | ((uint32_t)f2h(wt * acc[mb][4 * q + 1]) << 16);
+          v.y = (uint32_t)f2h(wt * acc[mb][4 * q + 2]) | ((uint32_t)f2h(wt * acc[mb][4 * q + 3]) << 16);
+          const int64_t c0 = (int64_t)t.ntile * 256 + wave * 32 + 8 * q + 4 * hh;
+          *reinterpret_cast<u32x2*>(contrib_out + row * H + c0) = v;
+        }
+      }
+    }
+  }
+}
 
 template <bool GATEUP>
 __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
     aima_moe_layer L, const uint16_t* __restrict__ src, const int32_t* __restrict__ tiles,
     const int32_t* __restrict__ tile_count, const int32_t* __restrict__ token_map,
     const float* __restrict__ row_weight, int64_t A, int ntiles_n,
-    uint16_t* __restrict__ act_out, float* __restrict__ contrib_out) {
-  // LDS: three stages of A tiles, weight bytes and scale / zero-point words,
-  // then the router weights of the tile's rows (down epilogue)
-  constexpr int kOffB = 3 * kStageA, kOffZ = kOffB + 3 * kStageB, kOffW = kOffZ + 3 * kStageSZ;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kOffW + kBM * 4];
-  const int total = *tile_count * ntiles_n;
-  const int per_xcd = (total + 7) / 8;
+    uint16_t* __restrict__ act_out, uint16_t* __restrict__ contrib_out) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
   const int p = blockIdx.x;
-  const int logical = (p % 8) * per_xcd + p / 8;
-  if (p / 8 >= per_xcd || logical >= total) return;
-  const int tile = logical / ntiles_n;
-  const int ntile = logical - tile * ntiles_n;
+  const int slot = p >> 3;
+  const int mt = (slot / ntiles_n) * 8 + (p & 7);
+  if (mt >= *tile_count) return;
 
-  const int e = tiles[4 * tile + 0];
-  const int64_t row0 = tiles[4 * tile + 1];
-  const int rows = tiles[4 * tile + 2];
-  const int E = L.experts;
+  GemmTile t;
+  t.ntile = slot % ntiles_n;
+  t.e = tiles[4 * mt + 0];
+  t.row0 = tiles[4 * mt + 1];
+  t.rows = tiles[4 * mt + 2];
+  t.E = L.experts;
   const int64_t H = L.hidden, I = L.inter;
   const int64_t K = GATEUP ? H : I;
-  const int GK = (int)(K / 128);
+  t.GK = (int)(K / 128);
+  t.S = (int)(K / kStageK);
   const int64_t rows_e = GATEUP ? 2 * I : H;
 
-  const aima_u4_tensor& W = GATEUP ? (e < E ? L.gate_up : L.shared_gate_up)
-                                   : (e < E ? L.down : L.shared_down);
-  const int64_t eoff = (e < E) ? e : 0;
+  const aima_u4_tensor& W = GATEUP ? (t.e < t.E ? L.gate_up : L.shared_gate_up)
+                                   : (t.e < t.E ? L.down : L.shared_down);
+  const int64_t eoff = (t.e < t.E) ? t.e : 0;
   const uint8_t* qw = W.qweight + eoff * rows_e * (K / 2);
-  const uint8_t* sc = reinterpret_cast<const uint8_t*>(W.scale + eoff * rows_e * GK);
-  const uint8_t* zp = W.zp + eoff * (rows_e * GK / 2);
+  const uint8_t* sc = reinterpret_cast<const uint8_t*>(W.scale + eoff * rows_e * t.GK);
+  const uint8_t* zp = W.zp + eoff * (rows_e * t.GK / 2);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int n = lane & 31, hh = lane >> 5;
-
-  // weight row of MFMA column n_ of column block w_
-  auto wrow = [&](int w_, int n_) -> int64_t {
+  // weight row of MFMA row i of wave w_
+  auto wrow = [&](int w_, int i) -> int64_t {
     if (GATEUP) {
-      const int64_t j = (int64_t)ntile * 128 + w_ * 16 + (n_ & 15);
-      return n_ < 16 ? j : I + j;
+      const int q = i >> 3;
+      const int64_t j = (int64_t)t.ntile * 128 + w_ * 16 + 8 * (q & 1) + (i & 7);
+      return q < 2 ? j : I + j;
     }
-    return (int64_t)ntile * 256 + w_ * 32 + n_;
+    return (int64_t)t.ntile * 256 + w_ * 32 + i;
   };
-  const int64_t my_row = wrow(wave, n);
+  t.my_row = wrow(wave, lane & 31);
 
-  // --- direct-load sources of this lane: uniform bases + 32-bit offsets ---
-  // A: block instruction q = 4 wave + i covers rows 4q .. 4q+3; lane -> row
-  // 4q + lane/16, LDS slot lane%16 holding piece (lane%16) ^ (row & 15).
-  // Rows past the tile read the tile's first row (valid memory; their
-  // results are never stored).  (Byte offsets stay below 2^31: the host
-  // limits tokens * hidden.)
-  const void* a_base = uniform_ptr(src);
-  uint32_t aoff[4];
+  // Token-row loads: load i of wave w is block instruction q = 8 i + w,
+  // covering rows 8 q .. 8 q + 7; lane -> row 8 q + lane / 8, LDS slot
+  // lane % 8 holding piece (lane % 8) ^ ((row >> 1) & 7).  Rows past the tile
+  // read the tile's first row (valid memory; their results are never
+  // stored).  (Byte offsets stay below 2^31: the host limits tokens * hidden
+  // and tokens * (k + 1) * inter.)
+  t.a_base = uniform_ptr(src);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int r = 4 * (4 * wave + i) + (lane >> 4);
-    const int64_t grow = row0 + (r < rows ? r : 0);
-    int64_t srow;
-    if (GATEUP) {
-      srow = (e < E) ? (int64_t)token_map[grow] : grow - A;
-    } else {
-      srow = grow;
-    }
-    const int piece = (lane & 15) ^ (r & 15);
-    aoff[i] = (uint32_t)((srow * K + piece * 8) * 2);
+    const int r = 8 * (8 * i + wave) + (lane >> 3);
+    const int64_t grow = t.row0 + (r < t.rows ? r : 0);
+    const int64_t srow = GATEUP ? ((t.e < t.E) ? (int64_t)token_map[grow] : grow - A) : grow;
+    const int piece = (lane & 7) ^ ((r >> 1) & 7);
+    t.aoff[i] = (uint32_t)((srow * K + piece * 8) * 2);
   }
-  // B: wave w loads its own column block: 16-byte piece t of the 32 bytes
-  // lane (n, hh) consumes (k 64 hh .. +64 of the group)
-  const void* b_base = uniform_ptr(qw);
-  const uint32_t boff = (uint32_t)(my_row * (K / 2) + hh * 32);
-  // scale / zero-point words: wave w loads word set w: scales for w < 4,
-  // zero points for w >= 4; lane -> word (w % 4) * 64 + lane of column block
-  // idx / 32, column idx % 32
-  int64_t sz_row;
+  // Weight bytes: lane (i, hh) loads the 16 bytes it consumes in a stage
+  // (k 32 hh .. +32 of the stage).
+  t.b_base = uniform_ptr(qw);
+  t.boff = (uint32_t)(t.my_row * (K / 2) + (lane >> 5) * 16);
+  // Scale / zero-point words: waves 0-3 load the scale words, waves 4-7 the
+  // zero-point words; lane -> word (w % 4) * 64 + lane, i.e. MFMA row idx % 32
+  // of wave idx / 32.
   {
     const int idx = (wave & 3) * 64 + lane;
-    sz_row = wrow(idx >> 5, idx & 31);
+    t.sz_row = wrow(idx >> 5, idx & 31);
   }
-  const bool sz_is_zero = wave >= 4;
-  const void* z_base = uniform_ptr(sz_is_zero ? zp : sc);
+  t.sz_is_zero = wave >= 4;
+  t.z_base = uniform_ptr(t.sz_is_zero ? (const void*)zp : (const void*)sc);
 
-  // LDS destinations: the LDS base address plus wave-uniform integer offsets
-  const uint32_t lds0 = lds_addr(smem);
-  auto issue = [&](int g, int st) {
-    const uint32_t la = lds0 + (uint32_t)(st * kStageA + wave * 4096);
-    const uint32_t lb = lds0 + (uint32_t)(kOffB + st * kStageB + wave * 2048);
-    const uint32_t lz = lds0 + (uint32_t)(kOffZ + st * kStageSZ + wave * 256);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) lds_load16(a_base, aoff[i] + g * 256, la + i * 1024);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) lds_load16(b_base, boff + g * 64 + t * 16, lb + t * 1024);
-    const int64_t gi = sz_row * GK + g;
-    const uint32_t zoff = sz_is_zero ? (uint32_t)((gi >> 1) & ~(int64_t)3)
-                                     : (uint32_t)((gi * 2) & ~(int64_t)3);
-    lds_load4(z_base, zoff, lz);
-  };
-
-  // M blocks that hold rows of the tile
-  const int mb_active = min(4, (rows + 31) / 32);
-  f32x16 acc[4];
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) acc[mb] = f32x16{};
-  const uint32_t magic = u4_magic();
-
-  auto compute = [&](int g, int st) {
-    const uint8_t* sA = smem + st * kStageA;
-    const uint8_t* sB = smem + kOffB + st * kStageB;
-    const uint32_t* sZ = reinterpret_cast<const uint32_t*>(smem + kOffZ + st * kStageSZ);
-    const int col = wave * 32 + n;  // word index within a set
-    const uint32_t sw = sZ[col];
-    const uint32_t zw = sZ[256 + col];
-    const int64_t gi = my_row * GK + g;
-    const uint32_t sbits = (sw >> ((gi & 1) * 16)) & 0xffffu;
-    const uint32_t z = (zw >> ((gi & 7) * 4)) & 0xfu;
-    const f16x2 s2 = as_h2(sbits * 0x00010001u);
-    const f16x2 ss2 = f16x2{s2.x, (_Float16)(s2.y * (_Float16)0.0625f)};
-    const f16x2 zz2 = as_h2((0x6400u | z) | ((0x6400u | (z << 4)) << 16));
-    u32x4 braw[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      braw[t] = *reinterpret_cast<const u32x4*>(sB + ((2 * wave + t) * 64 + lane) * 16);
-    }
-    auto afrag = [&](int mb, int j) {
-      const int m = mb * 32 + n;
-      const int slot = (hh * 8 + j) ^ (m & 15);
-      return *reinterpret_cast<const f16x8*>(sA + m * 256 + slot * 16);
-    };
-    // All four M blocks run unconditionally (rows past the tile hold valid
-    // copies of row 0 and are never stored): straight-line code in which the
-    // A fragments of k-step j+1 load and its weights dequantize while the
-    // MFMAs of step j run.
-    f16x8 af[2][4];
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb) af[0][mb] = afrag(mb, 0);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (j + 1 < 8) {
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb) af[(j + 1) & 1][mb] = afrag(mb, j + 1);
-      }
-      const f16x8 b = dequant8(braw[j >> 2][j & 3], zz2, ss2, magic);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[j & 1][mb], b, acc[mb], 0, 0, 0);
-      }
-    }
-  };
-
-  // Pipeline: groups g+1 and g+2 load while g computes.  Before computing g
-  // a wave waits for its own loads of g (those of g+1, issued later, may stay
-  // in flight), then the barrier makes every wave's loads of g visible and
-  // guarantees every wave is done with the stage that g+2 reuses.  The
-  // barrier is a plain s_barrier between compiler memory barriers: no fence,
-  // so it does not wait for the loads in flight.
-  auto sync_stage = [&](bool last) {
-    if (!last) {
-      asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-  };
-  static_assert(kLoadsPerStage == 7, "the vmcnt(7) above counts one stage's loads");
-  issue(0, 0);
-  if (GK > 1) issue(1, 1);
-  for (int g = 0, st = 0; g < GK; ++g, st = (st == 2 ? 0 : st + 1)) {
-    sync_stage(g + 1 >= GK);
-    if (g + 2 < GK) issue(g + 2, st == 0 ? 2 : st - 1);
-    compute(g, st);
-  }
-
-  // Epilogue.  32x32 MFMA output: lane holds column n, rows
-  // 8*(v/4) + 4*hh + (v%4) of its M block.  (down: the rows' router weights
-  // are staged in LDS first, one load per row)
-  float* s_wt = reinterpret_cast<float*>(smem + kOffW);
-  if (!GATEUP) {
-    if (tid < kBM) s_wt[tid] = (e < E && tid < rows) ? row_weight[row0 + tid] : 1.0f;
-    __syncthreads();
-  }
-#pragma unroll
-  for (int mb = 0; mb < 4; ++mb) {
-    if (mb < mb_active) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = mb * 32 + 8 * (v >> 2) + 4 * hh + (v & 3);
-        if (GATEUP) {
-          // gate in columns 0..15, up in 16..31 of the same lane half
-          const float other = __shfl_xor(acc[mb][v], 16, 64);
-          if (n < 16 && r < rows) {
-            act_out[(row0 + r) * I + my_row] = f2h(silu_mul(acc[mb][v], other));
-          }
-        } else if (r < rows) {
-          contrib_out[(row0 + r) * H + my_row] = s_wt[r] * acc[mb][v];
-        }
-      }
-    }
+  switch ((t.rows + 31) >> 5) {
+    case 1: gemm_tile<GATEUP, 1>(t, smem, L, row_weight, act_out, contrib_out); break;
+    case 2: gemm_tile<GATEUP, 2>(t, smem, L, row_weight, act_out, contrib_out); break;
+    case 3: gemm_tile<GATEUP, 3>(t, smem, L, row_weight, act_out, contrib_out); break;
+    case 4: gemm_tile<GATEUP, 4>(t, smem, L, row_weight, act_out, contrib_out); break;
+    case 5: gemm_tile<GATEUP, 5>(t, smem, L, row_weight, act_out, contrib_out); break;
+    case 6: gemm_tile<GATEUP, 6>(t, smem, L, row_weight, act_out, contrib_out); break;
+    case 7: gemm_tile<GATEUP, 7>(t, smem, L, row_weight, act_out, contrib_out); break;
+    default: gemm_tile<GATEUP, 8>(t, smem, L, row_weight, act_out, contrib_out); break;
   }
 }
 
@@ -587,8 +639,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
 // combine: out[t] = f16(residual[t] + (sum_r contrib[inv[t][r]] + sigma_t * shared[t]))
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void combine_kernel(
-    const float* __restrict__ contrib, const int32_t* __restrict__ inverse_map, int k, int64_t A,
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate_vec,
+    const uint16_t* __restrict__ contrib, const int32_t* __restrict__ inverse_map, int k,
+    int64_t A, const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate_vec,
     const uint16_t* __restrict__ residual, int64_t H, uint16_t* __restrict__ out) {
   __shared__ float red[4];
   __shared__ int rowsel[16];
@@ -600,24 +652,39 @@ __global__ __launch_bounds__(256) void combine_kernel(
   const float sigma = (float)(gd >= 0.0 ? 1.0 / (1.0 + exp(-gd)) : exp(gd) / (1.0 + exp(gd)));
   if (threadIdx.x < k) rowsel[threadIdx.x] = inverse_map[t * k + threadIdx.x];
   __syncthreads();
-  const float* shared_row = contrib + (A + t) * H;
-  for (int64_t h = threadIdx.x * 4; h < H; h += 1024) {
-    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  const uint16_t* shared_row = contrib + (A + t) * H;
+  for (int64_t h = threadIdx.x * 8; h < H; h += 2048) {
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     for (int r = 0; r < k; ++r) {
-      const float4 c = *reinterpret_cast<const float4*>(contrib + (int64_t)rowsel[r] * H + h);
-      s.x += c.x;
-      s.y += c.y;
-      s.z += c.z;
-      s.w += c.w;
+      const u32x4 c = *reinterpret_cast<const u32x4*>(contrib + (int64_t)rowsel[r] * H + h);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t wj = c[j];
+        s[2 * j] += h2f((uint16_t)(wj & 0xffffu));
+        s[2 * j + 1] += h2f((uint16_t)(wj >> 16));
+      }
     }
-    const float4 c = *reinterpret_cast<const float4*>(shared_row + h);
-    float o[4] = {s.x + c.x * sigma, s.y + c.y * sigma, s.z + c.z * sigma, s.w + c.w * sigma};
+    const u32x4 c = *reinterpret_cast<const u32x4*>(shared_row + h);
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t wj = c[j];
+      o[2 * j] = s[2 * j] + h2f((uint16_t)(wj & 0xffffu)) * sigma;
+      o[2 * j + 1] = s[2 * j + 1] + h2f((uint16_t)(wj >> 16)) * sigma;
+    }
     if (residual) {
+      const u32x4 rv = *reinterpret_cast<const u32x4*>(residual + t * H + h);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = h2f(residual[t * H + h + j]) + o[j];
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t wj = rv[j];
+        o[2 * j] = h2f((uint16_t)(wj & 0xffffu)) + o[2 * j];
+        o[2 * j + 1] = h2f((uint16_t)(wj >> 16)) + o[2 * j + 1];
+      }
     }
+    u32x4 ov;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) out[t * H + h + j] = f2h(o[j]);
+    for (int j = 0; j < 4; ++j) ov[j] = (uint32_t)f2h(o[2 * j]) | ((uint32_t)f2h(o[2 * j + 1]) << 16);
+    *reinterpret_cast<u32x4*>(out + t * H + h) = ov;
   }
 }
 
@@ -633,16 +700,18 @@ static int expert_bits(int E) {
 static int launch_schedule(const int32_t* ids, const float* weights, const PrefillDims& d,
                            const PrefillWs& w, hipStream_t st) {
   const int bits = expert_bits(d.E);
-  hipLaunchKernelGGL(sched_count_kernel, dim3((unsigned)d.nb), dim3(64), 0, st, ids, d.A, d.k,
-                     d.E, bits, w.err, w.block_base);
+  int Ep = 1;
+  while (Ep < d.E) Ep <<= 1;
+  hipLaunchKernelGGL(sched_count_kernel, dim3((unsigned)d.nb), dim3(kSchedBlock), 0, st, ids,
+                     (int32_t)d.A, d.k, d.E, bits, w.err, w.block_base, w.inverse_map);
   int rc = launch_check("grouped schedule count");
   if (rc != AIMA_OK) return rc;
-  hipLaunchKernelGGL(sched_scan_kernel, dim3(1), dim3(1024), 0, st, w.block_base, d.nb, d.E, d.T,
-                     d.A, w.offsets, w.tiles, w.tile_count);
+  hipLaunchKernelGGL(sched_scan_kernel, dim3(1), dim3(1024), 0, st, w.block_base, (int32_t)d.nb,
+                     d.E, Ep, (int32_t)d.T, (int32_t)d.A, w.offsets, w.tiles, w.tile_count);
   rc = launch_check("grouped schedule scan");
   if (rc != AIMA_OK) return rc;
-  hipLaunchKernelGGL(sched_scatter_kernel, dim3((unsigned)d.nb), dim3(64), 0, st, ids, weights,
-                     d.A, d.k, d.E, bits, w.block_base, w.token_map, w.inverse_map,
+  hipLaunchKernelGGL(sched_scatter_kernel, dim3((unsigned)d.nb), dim3(kSchedBlock), 0, st, ids,
+                     weights, (int32_t)d.A, d.k, d.E, w.block_base, w.token_map, w.inverse_map,
                      w.row_weight);
   return launch_check("grouped schedule scatter");
 }
@@ -652,20 +721,19 @@ static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint1
                          const PrefillDims& d, const PrefillWs& w, hipStream_t st) {
   int rc = launch_schedule(ids, weights, d, w, st);
   if (rc != AIMA_OK) return rc;
+  const unsigned mtiles = (unsigned)round_up(d.max_tiles, 8);
   {
     const int nt = d.I / 128;
-    const unsigned grid = (unsigned)round_up(d.max_tiles * nt, 8);
-    hipLaunchKernelGGL((grouped_gemm_kernel<true>), dim3(grid), dim3(kGemmThreads), 0, st, L, x,
-                       w.tiles, w.tile_count, w.token_map, w.row_weight, d.A, nt, w.act,
+    hipLaunchKernelGGL((grouped_gemm_kernel<true>), dim3(mtiles * nt), dim3(kGemmThreads), 0, st,
+                       L, x, w.tiles, w.tile_count, w.token_map, w.row_weight, d.A, nt, w.act,
                        w.contrib);
   }
   rc = launch_check("grouped gate/up GEMM");
   if (rc != AIMA_OK) return rc;
   {
     const int nt = d.H / 256;
-    const unsigned grid = (unsigned)round_up(d.max_tiles * nt, 8);
-    hipLaunchKernelGGL((grouped_gemm_kernel<false>), dim3(grid), dim3(kGemmThreads), 0, st, L,
-                       w.act, w.tiles, w.tile_count, w.token_map, w.row_weight, d.A, nt, w.act,
+    hipLaunchKernelGGL((grouped_gemm_kernel<false>), dim3(mtiles * nt), dim3(kGemmThreads), 0, st,
+                       L, w.act, w.tiles, w.tile_count, w.token_map, w.row_weight, d.A, nt, w.act,
                        w.contrib);
   }
   rc = launch_check("grouped down GEMM");
