@@ -342,7 +342,7 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d, f16x2 zz2, f16x2 ss2, uint
   return __builtin_bit_cast(f16x8, v);
 }
 
-// Direct global -> LDS loads (each lane's 16 or 4 bytes land at the
+// Direct global -> LDS loads (each lane's 16 bytes land at the
 // wave-uniform LDS address + lane * size), addressed as a wave-uniform base
 // (SGPRs) plus a 32-bit per-lane byte offset.  Issued through inline
 // assembly: the compiler then neither counts them nor orders LDS reads behind
@@ -362,20 +362,6 @@ __device__ __forceinline__ void lds_load16(const void* base, uint32_t off, uint3
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds)
                : "memory");
 }
-__device__ __forceinline__ void lds_load4(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds)
-               : "memory");
-}
-// Waits until at most N of this wave's vector memory operations are pending.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N <= 6, "vmcnt immediate");
-  if constexpr (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-  if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-  if constexpr (N == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
-  if constexpr (N == 6) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-}
 // Block barrier that does not wait for outstanding memory operations (the
 // waves wait for their own loads first).
 __device__ __forceinline__ void plain_barrier() {
@@ -390,48 +376,48 @@ __device__ __forceinline__ void plain_barrier() {
 // weight rows and every token row of the tile.  The weights are the MFMA A
 // operand (lane l dequantizes weight row l % 32, 8 k values per k-step) and
 // the token rows the B operand (MFMA block mb = token rows 32 mb .. +32), so
-// each dequantized weight feeds MB MFMAs, and the 32x32 result leaves lane
+// each dequantized weight feeds MB MFMAs.  The 32x32 result leaves lane
 // (n, hh) with 4 consecutive weight rows 8 q + 4 hh .. +3 (q = 0..3) of token
-// row n: the epilogue stores 8-byte runs of output columns.  For gate/up the
-// 32 weight rows of a wave are arranged so that q = 0, 1 are gate rows and
-// q = 2, 3 the up rows of the same 16 columns; SwiGLU needs no lane exchange.
+// row n.  For gate/up the 32 weight rows of a wave are arranged so that
+// q = 0, 1 are gate rows and q = 2, 3 the up rows of the same 16 columns;
+// SwiGLU needs no lane exchange.
 //
-// The K loop runs in stages of 64 (half a quantization group).  All operands
-// of a stage reach LDS by direct global->LDS loads, three stages in flight:
-// the token rows (256 rows x 128 bytes, gathered through the token map;
-// 16-byte piece p of row r sits in slot p ^ ((r >> 1) & 7), which keeps MFMA
-// operand reads free of bank conflicts), each wave's packed weight bytes
-// (32 rows x 32 bytes, in lane order) and the rows' scale and zero-point
-// words.  MB (1..8) is the tile height in 32-row blocks: rows past the tile
-// are neither loaded (beyond the MB blocks) nor multiplied.
+// The K loop runs over the 128-wide quantization groups.  Each lane loads
+// the packed bytes, scale and zero point of its own weight row straight into
+// registers one group ahead.  The token rows of a group (256 rows x 256
+// bytes, gathered through the token map) reach LDS by direct global->LDS
+// loads into a two-buffer ring; 16-byte piece p of row r sits in slot
+// p ^ (r & 15), which keeps the MFMA operand reads free of bank conflicts.
+// MB (1..8) is the tile height in 32-row blocks: rows past the tile are
+// neither loaded (beyond the MB blocks) nor multiplied.  The epilogue stages
+// the output tile in LDS and writes whole rows with 16-byte stores.
 //
 // Blocks are mapped XCD-aware: physical block p runs on XCD p % 8
 // (round-robin dispatch); M tile i goes to XCD i % 8 and the N tiles of one M
 // tile (same token rows) are consecutive on that XCD, so they share its L2.
 // Tiles come tallest first, so each XCD works through large tiles first.
 constexpr int kGemmThreads = 512;
-constexpr int kStageK = 64;                   // K per pipeline stage
-constexpr int kStageA = kBM * kStageK * 2;    // token rows, bytes
-constexpr int kStageB = 256 * kStageK / 2;    // packed weights, bytes
-constexpr int kStageSZ = 2 * 256 * 4;         // scale and zero-point words
-constexpr int kOffB = 3 * kStageA;
-constexpr int kOffZ = kOffB + 3 * kStageB;
-constexpr int kSmemBytes = kOffZ + 3 * kStageSZ;
+constexpr int kStageA = kBM * 128 * 2;   // token rows of one group, bytes
+constexpr int kSmemBytes = 2 * kStageA;  // two-buffer ring; the epilogue reuses it
 
 struct GemmTile {
-  const void* a_base;   // token rows (uniform)
-  const void* b_base;   // packed weights of the expert (uniform)
-  const void* z_base;   // scale or zero-point words (uniform)
-  uint32_t aoff[4];     // per-lane byte offsets of the token-row pieces
-  uint32_t boff;        // per-lane byte offset of the weight bytes
-  int64_t sz_row;       // weight row whose scale / zero word this lane loads
-  int64_t my_row;       // weight row this lane dequantizes
-  int GK, S;            // quantization groups, stages
+  const void* a_base;     // token rows (uniform)
+  const uint8_t* wq;      // this lane's packed weight row (+ its k half)
+  const uint16_t* ws;     // this lane's scale row
+  const uint8_t* wz;      // packed zero points of the expert
+  uint32_t aoff[8];       // per-lane byte offsets of the token-row pieces
+  int64_t zbase;          // this lane's zero-point index (row * GK)
+  int GK;                 // quantization groups along K
   int e, E, rows;
   int64_t row0;
   int ntile;
-  bool sz_is_zero;
 };
+
+// silu(g) * u with the hardware exp and reciprocal (relative error ~1e-7;
+// exp(-g) = inf for very negative g gives 0, as it should).
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+  return g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
 
 template <bool GATEUP, int MB>
 __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
@@ -439,112 +425,177 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
                                           const float* __restrict__ row_weight,
                                           uint16_t* __restrict__ act_out,
                                           uint16_t* __restrict__ contrib_out) {
-  constexpr int NA = (MB + 1) / 2;   // token-row loads per wave per stage
-  constexpr int NL = NA + 2;         // + weight bytes + scale / zero word
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, hh = lane >> 5;
   const uint32_t lds0 = lds_addr(smem);
 
-  auto issue = [&](int s, int st) {
-    const uint32_t la = lds0 + (uint32_t)(st * kStageA + wave * 1024);
+  // token rows of group g into buffer st: wave w issues block instructions
+  // q = w + 8 i (rows 4 q .. 4 q + 3), i < MB
+  auto issue = [&](int g, int st) {
 #pragma unroll
-    for (int i = 0; i < NA; ++i) lds_load16(t.a_base, t.aoff[i] + s * 128, la + i * 8192);
-    lds_load16(t.b_base, t.boff + s * 32, lds0 + (uint32_t)(kOffB + st * kStageB + wave * 1024));
-    const int64_t gi = t.sz_row * t.GK + (s >> 1);
-    const uint32_t zoff = t.sz_is_zero ? (uint32_t)((gi >> 1) & ~(int64_t)3)
-                                       : (uint32_t)((gi * 2) & ~(int64_t)3);
-    lds_load4(t.z_base, zoff, lds0 + (uint32_t)(kOffZ + st * kStageSZ + wave * 256));
+    for (int i = 0; i < MB; ++i) {
+      lds_load16(t.a_base, t.aoff[i] + g * 256,
+                 lds0 + (uint32_t)(st * kStageA + (wave + 8 * i) * 1024));
+    }
+  };
+  struct WGroup {
+    u32x4 q0, q1;    // 64 nibbles: k 64 hh .. +64 of the group
+    uint32_t s, z;   // f16 scale bits, zero-point byte
+  };
+  auto load_w = [&](int g) {
+    WGroup r;
+    r.q0 = *reinterpret_cast<const u32x4*>(t.wq + g * 64);
+    r.q1 = *reinterpret_cast<const u32x4*>(t.wq + g * 64 + 16);
+    r.s = t.ws[g];
+    r.z = t.wz[(t.zbase + g) >> 1];
+    return r;
   };
 
   f32x16 acc[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
   const uint32_t magic = u4_magic();
-  const int swz = (n >> 1) & 7;  // token row m = 32 mb + n: (m >> 1) & 7
 
-  auto compute = [&](int s, int st) {
-    const uint8_t* sA = smem + st * kStageA;
-    const uint32_t* sZ = reinterpret_cast<const uint32_t*>(smem + kOffZ + st * kStageSZ);
-    const int col = wave * 32 + n;
-    const uint32_t sw = sZ[col];
-    const uint32_t zw = sZ[256 + col];
-    const int64_t gi = t.my_row * t.GK + (s >> 1);
-    const uint32_t sbits = (sw >> ((gi & 1) * 16)) & 0xffffu;
-    const uint32_t z = (zw >> ((gi & 7) * 4)) & 0xfu;
-    const f16x2 s2 = as_h2(sbits * 0x00010001u);
+  // sA: the group's token rows in LDS, row m at sA + 256 m
+  auto compute = [&](int g, const uint8_t* sA, const WGroup& w) {
+    const uint32_t z = (w.z >> (((t.zbase + g) & 1) * 4)) & 0xfu;
+    const f16x2 s2 = as_h2(w.s * 0x00010001u);
     const f16x2 ss2 = f16x2{s2.x, (_Float16)(s2.y * (_Float16)0.0625f)};
     const f16x2 zz2 = as_h2((0x6400u | z) | ((0x6400u | (z << 4)) << 16));
-    const u32x4 braw =
-        *reinterpret_cast<const u32x4*>(smem + kOffB + st * kStageB + wave * 1024 + lane * 16);
     auto bfrag = [&](int mb, int j) {
-      const int slot = (hh * 4 + j) ^ swz;
-      return *reinterpret_cast<const f16x8*>(sA + (mb * 32 + n) * 128 + slot * 16);
+      const int m = mb * 32 + n;
+      const int slot = (hh * 8 + j) ^ (m & 15);
+      return *reinterpret_cast<const f16x8*>(sA + m * 256 + slot * 16);
     };
+    auto wword = [&](int j) { return j < 4 ? w.q0[j & 3] : w.q1[j & 3]; };
+    // Software pipeline over the 8 k-steps: step j issues the operand reads
+    // and the dequantization of step j+1, then its MB independent MFMAs (one
+    // per accumulator).  The scheduling fences keep each step's MFMAs
+    // together: left alone, the scheduler runs all k-steps of one accumulator
+    // back to back, and each MFMA then waits for the previous one's result.
     f16x8 bf[2][MB];
+    f16x8 a[2];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) bf[0][mb] = bfrag(mb, 0);
+    a[0] = dequant8(wword(0), zz2, ss2, magic);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (j + 1 < 4) {
+    for (int j = 0; j < 8; ++j) {
+      if (j + 1 < 8) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) bf[(j + 1) & 1][mb] = bfrag(mb, j + 1);
+        a[(j + 1) & 1] = dequant8(wword(j + 1), zz2, ss2, magic);
       }
-      const f16x8 a = dequant8(braw[j], zz2, ss2, magic);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bf[j & 1][mb], acc[mb], 0, 0, 0);
+        acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[j & 1], bf[j & 1][mb], acc[mb], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Pipeline: stages s+1 and s+2 load while s computes.  Before computing s a
-  // wave waits for its own loads of s (those of s+1, issued later, may stay
-  // in flight), then the barrier makes every wave's loads of s visible and
-  // guarantees every wave is done with the buffer that s+2 reuses.
-  const int S = t.S;
-  issue(0, 0);
-  issue(1, 1);
-  for (int s = 0, st = 0; s < S; ++s, st = (st == 2 ? 0 : st + 1)) {
-    if (s + 1 < S) {
-      wait_vmcnt<NL>();
-    } else {
-      wait_vmcnt<0>();
+
+  const int GK = t.GK;
+  constexpr int kResidentGroupBytes = MB * 32 * 256;  // token rows of one group
+  if (GK * kResidentGroupBytes <= kSmemBytes) {
+    // The tile's token rows for the whole K fit in LDS: load them once, one
+    // barrier, then every group runs without block synchronization (the
+    // waves drift apart, which overlaps one wave's dequantization with
+    // another's MFMAs).  Weights stream into registers two groups ahead.
+    for (int g = 0; g < GK; ++g) {
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        lds_load16(t.a_base, t.aoff[i] + g * 256,
+                   lds0 + (uint32_t)(g * kResidentGroupBytes + (wave + 8 * i) * 1024));
+      }
     }
+    WGroup w0 = load_w(0);
+    WGroup w1 = GK > 1 ? load_w(1) : w0;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     plain_barrier();
-    if (s + 2 < S) issue(s + 2, st == 0 ? 2 : st - 1);
-    compute(s, st);
+    for (int g = 0; g < GK; ++g) {
+      const WGroup w = w0;
+      w0 = w1;
+      if (g + 2 < GK) w1 = load_w(g + 2);
+      compute(g, smem + g * kResidentGroupBytes, w);
+    }
+  } else {
+    // Pipeline: group g+1 loads (token rows into the other buffer, weights
+    // into registers) while g computes.  Each iteration first waits for all
+    // of this wave's loads (those of g), then the barrier makes every wave's
+    // token rows of g visible and guarantees every wave is done with the
+    // buffer that g+1 refills.  The barrier itself does not wait for memory.
+    issue(0, 0);
+    WGroup wn = load_w(0);
+    for (int g = 0; g < GK; ++g) {
+      const int st = g & 1;
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      plain_barrier();
+      const WGroup w = wn;
+      if (g + 1 < GK) {
+        issue(g + 1, st ^ 1);
+        wn = load_w(g + 1);
+      }
+      compute(g, smem + st * kStageA, w);
+    }
   }
 
   // Epilogue: lane (n, hh) of MFMA block mb holds token row m = 32 mb + n and
-  // weight rows 8 q + 4 hh + c in acc[mb][4 q + c].
+  // weight rows 8 q + 4 hh + c in acc[mb][4 q + c].  Each lane writes its
+  // 8-byte runs into an LDS copy of the output tile (16-byte chunk j of row m
+  // at chunk slot j ^ (m % chunks)), then whole rows go out as 16-byte stores.
   const int64_t H = L.hidden, I = L.inter;
+  constexpr int kChunks = GATEUP ? 16 : 32;   // 16-byte chunks per tile row
+  constexpr int kRowBytes = kChunks * 16;
+  float wt[MB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = mb * 32 + n;
-    if (m < t.rows) {
-      const int64_t row = t.row0 + m;
-      if (GATEUP) {
+    wt[mb] = (!GATEUP && t.e < t.E && m < t.rows) ? row_weight[t.row0 + m] : 1.0f;
+  }
+  __syncthreads();  // every wave is done with the token-row buffers
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          u32x2 v;
-          v.x = (uint32_t)f2h(silu_mul(acc[mb][4 * q + 0], acc[mb][8 + 4 * q + 0])) |
-                ((uint32_t)f2h(silu_mul(acc[mb][4 * q + 1], acc[mb][8 + 4 * q + 1])) << 16);
-          v.y = (uint32_t)f2h(silu_mul(acc[mb][4 * q + 2], acc[mb][8 + 4 * q + 2])) |
-                ((uint32_t)f2h(silu_mul(acc[mb][4 * q + 3], acc[mb][8 + 4 * q + 3])) << 16);
-          const int64_t c0 = (int64_t)t.ntile * 128 + wave * 16 + 8 * q + 4 * hh;
-          *reinterpret_cast<u32x2*>(act_out + row * I + c0) = v;
-        }
-      } else {
-        const float wt = t.e < t.E ? row_weight[row] : 1.0f;
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = mb * 32 + n;
+    uint8_t* rowp = smem + m * kRowBytes;
+    if (GATEUP) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          u32x2 v;
-          v.x = (uint32_t)f2h(wt * acc[mb][4 * q + 0]) | ((uint32_t)f2h(wt * acc[mb][4 * q + 1]) << 16);
-          v.y = (uint32_t)f2h(wt * acc[mb][4 * q + 2]) | ((uint32_t)f2h(wt * acc[mb][4 * q + 3]) << 16);
-          const int64_t c0 = (int64_t)t.ntile * 256 + wave * 32 + 8 * q + 4 * hh;
-          *reinterpret_cast<u32x2*>(contrib_out + row * H + c0) = v;
-        }
+      for (int q = 0; q < 2; ++q) {
+        u32x2 v;
+        v.x = (uint32_t)f2h(silu_mul_fast(acc[mb][4 * q + 0], acc[mb][8 + 4 * q + 0])) |
+              ((uint32_t)f2h(silu_mul_fast(acc[mb][4 * q + 1], acc[mb][8 + 4 * q + 1])) << 16);
+        v.y = (uint32_t)f2h(silu_mul_fast(acc[mb][4 * q + 2], acc[mb][8 + 4 * q + 2])) |
+              ((uint32_t)f2h(silu_mul_fast(acc[mb][4 * q + 3], acc[mb][8 + 4 * q + 3])) << 16);
+        const int chunk = (wave * 2 + q) ^ (m & (kChunks - 1));
+        *reinterpret_cast<u32x2*>(rowp + chunk * 16 + hh * 8) = v;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        u32x2 v;
+        v.x = (uint32_t)f2h(wt[mb] * acc[mb][4 * q + 0]) |
+              ((uint32_t)f2h(wt[mb] * acc[mb][4 * q + 1]) << 16);
+        v.y = (uint32_t)f2h(wt[mb] * acc[mb][4 * q + 2]) |
+              ((uint32_t)f2h(wt[mb] * acc[mb][4 * q + 3]) << 16);
+        const int chunk = (wave * 4 + q) ^ (m & (kChunks - 1));
+        *reinterpret_cast<u32x2*>(rowp + chunk * 16 + hh * 8) = v;
+      }
+    }
+  }
+  __syncthreads();
+  {
+    const int c = tid % kChunks;
+    constexpr int kRowsPerPass = kGemmThreads / kChunks;
+    uint16_t* out = GATEUP ? act_out : contrib_out;
+    const int64_t ld = GATEUP ? I : H;
+    const int64_t col0 = (int64_t)t.ntile * (GATEUP ? 128 : 256) + c * 8;
+#pragma unroll
+    for (int i = 0; i < MB * 32 / kRowsPerPass; ++i) {
+      const int m = tid / kChunks + kRowsPerPass * i;
+      if (m < t.rows) {
+        const u32x4 v =
+            *reinterpret_cast<const u32x4*>(smem + m * kRowBytes + ((c ^ (m & (kChunks - 1))) * 16));
+        *reinterpret_cast<u32x4*>(out + (t.row0 + m) * ld + col0) = v;
       }
     }
   }
@@ -571,57 +622,47 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
   const int64_t H = L.hidden, I = L.inter;
   const int64_t K = GATEUP ? H : I;
   t.GK = (int)(K / 128);
-  t.S = (int)(K / kStageK);
   const int64_t rows_e = GATEUP ? 2 * I : H;
 
   const aima_u4_tensor& W = GATEUP ? (t.e < t.E ? L.gate_up : L.shared_gate_up)
                                    : (t.e < t.E ? L.down : L.shared_down);
   const int64_t eoff = (t.e < t.E) ? t.e : 0;
-  const uint8_t* qw = W.qweight + eoff * rows_e * (K / 2);
-  const uint8_t* sc = reinterpret_cast<const uint8_t*>(W.scale + eoff * rows_e * t.GK);
-  const uint8_t* zp = W.zp + eoff * (rows_e * t.GK / 2);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  // weight row of MFMA row i of wave w_
-  auto wrow = [&](int w_, int i) -> int64_t {
+  // weight row (within the expert) of MFMA row i = lane % 32 of this wave
+  int64_t my_row;
+  {
+    const int i = lane & 31;
     if (GATEUP) {
       const int q = i >> 3;
-      const int64_t j = (int64_t)t.ntile * 128 + w_ * 16 + 8 * (q & 1) + (i & 7);
-      return q < 2 ? j : I + j;
+      const int64_t j = (int64_t)t.ntile * 128 + wave * 16 + 8 * (q & 1) + (i & 7);
+      my_row = q < 2 ? j : I + j;
+    } else {
+      my_row = (int64_t)t.ntile * 256 + wave * 32 + i;
     }
-    return (int64_t)t.ntile * 256 + w_ * 32 + i;
-  };
-  t.my_row = wrow(wave, lane & 31);
+  }
+  const int64_t wrow = eoff * rows_e + my_row;
+  t.wq = W.qweight + wrow * (K / 2) + (lane >> 5) * 32;
+  t.ws = W.scale + wrow * t.GK;
+  t.wz = W.zp;
+  t.zbase = wrow * t.GK;
 
-  // Token-row loads: load i of wave w is block instruction q = 8 i + w,
-  // covering rows 8 q .. 8 q + 7; lane -> row 8 q + lane / 8, LDS slot
-  // lane % 8 holding piece (lane % 8) ^ ((row >> 1) & 7).  Rows past the tile
+  // Token-row loads: block instruction q covers rows 4 q .. 4 q + 3; lane ->
+  // row 4 q + lane / 16, LDS slot lane % 16 holding piece
+  // (lane % 16) ^ (row & 15).  Wave w issues q = w + 8 i.  Rows past the tile
   // read the tile's first row (valid memory; their results are never
   // stored).  (Byte offsets stay below 2^31: the host limits tokens * hidden
   // and tokens * (k + 1) * inter.)
   t.a_base = uniform_ptr(src);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = 8 * (8 * i + wave) + (lane >> 3);
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * (wave + 8 * i) + (lane >> 4);
     const int64_t grow = t.row0 + (r < t.rows ? r : 0);
     const int64_t srow = GATEUP ? ((t.e < t.E) ? (int64_t)token_map[grow] : grow - A) : grow;
-    const int piece = (lane & 7) ^ ((r >> 1) & 7);
+    const int piece = (lane & 15) ^ (r & 15);
     t.aoff[i] = (uint32_t)((srow * K + piece * 8) * 2);
   }
-  // Weight bytes: lane (i, hh) loads the 16 bytes it consumes in a stage
-  // (k 32 hh .. +32 of the stage).
-  t.b_base = uniform_ptr(qw);
-  t.boff = (uint32_t)(t.my_row * (K / 2) + (lane >> 5) * 16);
-  // Scale / zero-point words: waves 0-3 load the scale words, waves 4-7 the
-  // zero-point words; lane -> word (w % 4) * 64 + lane, i.e. MFMA row idx % 32
-  // of wave idx / 32.
-  {
-    const int idx = (wave & 3) * 64 + lane;
-    t.sz_row = wrow(idx >> 5, idx & 31);
-  }
-  t.sz_is_zero = wave >= 4;
-  t.z_base = uniform_ptr(t.sz_is_zero ? (const void*)zp : (const void*)sc);
 
   switch ((t.rows + 31) >> 5) {
     case 1: gemm_tile<GATEUP, 1>(t, smem, L, row_weight, act_out, contrib_out); break;
