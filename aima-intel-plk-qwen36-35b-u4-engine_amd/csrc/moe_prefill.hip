@@ -177,32 +177,45 @@ __global__ __launch_bounds__(kSchedBlock) void sched_count_kernel(
   }
 }
 
-// Exclusive scan over the 1024 threads of a block; returns the prefix and
-// writes the grand total to *total.
-__device__ int block_exclusive_scan_1024(int v, int* smem, int* total) {
+// Exclusive scans of N values per thread over the 1024 threads of a block
+// at once: v[i] becomes the sum of v[i] over the earlier threads, tot[i] the
+// sum over all threads.  `smem` holds 17 * N ints.
+template <int N>
+__device__ void block_exclusive_scan_1024(int (&v)[N], int (&tot)[N], int* smem) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int inc = v;
+  int inc[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) inc[i] = v[i];
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(inc, off, 64);
-    if (lane >= off) inc += t;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const int t = __shfl_up(inc[i], off, 64);
+      if (lane >= off) inc[i] += t;
+    }
   }
-  if (lane == 63) smem[wave] = inc;
+  if (lane == 63) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) smem[wave * N + i] = inc[i];
+  }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  // lane i of wave 0 turns column i into exclusive wave prefixes + total
+  if (threadIdx.x < N) {
     int run = 0;
     for (int w = 0; w < 16; ++w) {
-      const int t = smem[w];
-      smem[w] = run;
-      run += t;
+      const int x = smem[w * N + threadIdx.x];
+      smem[w * N + threadIdx.x] = run;
+      run += x;
     }
-    smem[16] = run;
+    smem[16 * N + threadIdx.x] = run;
   }
   __syncthreads();
-  const int r = smem[wave] + inc - v;
-  *total = smem[16];
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    v[i] = smem[wave * N + i] + inc[i] - v[i];
+    tot[i] = smem[16 * N + i];
+  }
   __syncthreads();
-  return r;
 }
 
 // Tiles of one expert with `total` rows in class c (1..8 MFMA blocks of 32
@@ -214,30 +227,6 @@ __device__ __forceinline__ int tiles_in_class(int total, int c) {
   return (c == kTileClasses ? total / kBM : 0) + (cls == c ? 1 : 0);
 }
 
-// Writes the class-c tiles of one expert starting at tile index `at`.
-__device__ __forceinline__ void write_tiles(int32_t* __restrict__ tiles, int at, int c, int e,
-                                            int begin, int total) {
-  const int full = total / kBM, rem = total % kBM;
-  const int cls = (rem + 31) / 32;
-  int t = at;
-  if (c == kTileClasses) {
-    for (int i = 0; i < full; ++i, ++t) {
-      int32_t* td = tiles + 4 * (int64_t)t;
-      td[0] = e;
-      td[1] = begin + i * kBM;
-      td[2] = kBM;
-      td[3] = 0;
-    }
-  }
-  if (cls == c) {
-    int32_t* td = tiles + 4 * (int64_t)t;
-    td[0] = e;
-    td[1] = begin + full * kBM;
-    td[2] = rem;
-    td[3] = 0;
-  }
-}
-
 // One block of 1024 threads: thread (p, e) with e = tid % Ep (Ep = E rounded
 // up to a power of two) scans chunk p of expert e's block counts, the chunk
 // partial sums are combined through LDS, and the experts' totals are scanned
@@ -247,7 +236,7 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
                                                           int32_t A, int32_t* __restrict__ offsets,
                                                           int32_t* __restrict__ tiles,
                                                           int32_t* __restrict__ tile_count) {
-  __shared__ int smem[32];
+  __shared__ int smem[17 * (1 + kTileClasses)];
   __shared__ int part[1024];
   const int tid = threadIdx.x;
   const int e = tid % Ep, pidx = tid / Ep, P = 1024 / Ep;
@@ -272,11 +261,16 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
     total += v;
   }
   const bool rep = pidx == 0 && e < E;
-  int all_rows;
-  const int begin = block_exclusive_scan_1024(rep ? total : 0, smem, &all_rows);
+  // one scan for the row offsets and the tile counts of every class
+  // (v[0] rows, v[c] tiles of class c)
+  int v[1 + kTileClasses], tot[1 + kTileClasses];
+  v[0] = rep ? total : 0;
+#pragma unroll
+  for (int c = 1; c <= kTileClasses; ++c) v[c] = rep ? tiles_in_class(total, c) : 0;
+  block_exclusive_scan_1024<1 + kTileClasses>(v, tot, smem);
+  const int begin = v[0];
   if (rep) offsets[e] = begin + total;
   // expert e's row base reaches every chunk thread through LDS
-  __syncthreads();
   if (pidx == 0) part[e] = begin;
   __syncthreads();
   if (e < E) {
@@ -292,19 +286,48 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
       }
     }
   }
-  // tiles, by class (tallest first); the shared expert's tiles follow the
-  // routed ones of each class
-  int cbase = 0;
+  // Tiles, by class (tallest first); the shared expert's tiles follow the
+  // routed ones of each class.  An expert has full tiles (class 8) and at
+  // most one remainder tile of class ceil(rem / 32).
+  int cbase[kTileClasses + 1];
+  int all_tiles = 0;
+#pragma unroll
   for (int c = kTileClasses; c >= 1; --c) {
-    int routed;
-    const int n = rep ? tiles_in_class(total, c) : 0;
-    const int at = block_exclusive_scan_1024(n, smem, &routed);
-    if (rep && n) write_tiles(tiles, cbase + at, c, e, begin, total);
-    const int ns = tiles_in_class(T, c);
-    if (tid == 0 && ns) write_tiles(tiles, cbase + routed, c, E, A, T);
-    cbase += routed + ns;
+    cbase[c] = all_tiles;
+    all_tiles += tot[c] + tiles_in_class(T, c);
   }
-  if (tid == 0) *tile_count = cbase;
+  auto place = [&](int ex, int row_begin, int rows_total, int first8, int rem_pos_if_not8) {
+    const int full = rows_total / kBM, rem = rows_total % kBM;
+    for (int i = 0; i < full; ++i) {
+      int32_t* td = tiles + 4 * (int64_t)(first8 + i);
+      td[0] = ex;
+      td[1] = row_begin + i * kBM;
+      td[2] = kBM;
+      td[3] = 0;
+    }
+    if (rem) {
+      const int at = (rem + 31) / 32 == kTileClasses ? first8 + full : rem_pos_if_not8;
+      int32_t* td = tiles + 4 * (int64_t)at;
+      td[0] = ex;
+      td[1] = row_begin + full * kBM;
+      td[2] = rem;
+      td[3] = 0;
+    }
+  };
+  auto rem_slot = [&](int rows_total, const int (&prefix)[1 + kTileClasses]) {
+    const int cls = (rows_total % kBM + 31) / 32;
+    int pos = 0;
+#pragma unroll
+    for (int c = 1; c < kTileClasses; ++c) {
+      if (c == cls) pos = cbase[c] + prefix[c];
+    }
+    return pos;
+  };
+  if (rep) place(e, begin, total, cbase[kTileClasses] + v[kTileClasses], rem_slot(total, v));
+  if (tid == 0) {
+    place(E, A, T, cbase[kTileClasses] + tot[kTileClasses], rem_slot(T, tot));
+    *tile_count = all_tiles;
+  }
 }
 
 // One thread per assignment: the row = block base of its expert + its local
