@@ -178,6 +178,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="only the headline decode step (for profiling runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the config 2 grouped prefill (one layer, T=2048), timed with "
+                         "--steps launches; prints its JSON entry (for profiling runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (PMC counter "
                          "calibration) and exit")
@@ -207,6 +210,13 @@ def main():
     from aima_u4moe import ops, synth  # noqa: E402
 
     dev = torch.device("cuda:0")
+    if args.prefill_only:
+        layer = synth.moe_layer(hidden=H, inter=I, experts=E, group=GROUP, seed=4000, device=dev)
+        layers_c = ops._layers_c([layer])
+        res = prefill_config2(torch, pkg, ops, synth, layer, layers_c, dev, args.steps,
+                              args.warmup)
+        print(json.dumps({"prefill_config2_T2048": res}), flush=True)
+        return
     log(f"device {torch.cuda.get_device_name(0)}; building 40-layer stack")
     t0 = time.perf_counter()
     layers = [synth.moe_layer(hidden=H, inter=I, experts=E, group=GROUP, seed=4000 + l,
@@ -298,11 +308,9 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def prefill_bench(torch, pkg, ops, synth, layers, layers_c, dev):
-    out = {}
-    # config 2: one layer, T=2048, Zipf(1.1)-skewed routing
+def prefill_config2(torch, pkg, ops, synth, layer, layers_c, dev, iters=50, warmup=5):
+    """Config 2: one layer, T=2048, Zipf(1.1)-skewed routing."""
     T = 2048
-    layer = layers[0]
     x = synth.activations(T, H, 2, dev)
     ids, w = ops.select_router_topk(synth.router_logits(T, E, 3, dev, zipf_s=1.1), K_TOP)
     ws = ops.Workspace(dev)
@@ -317,19 +325,24 @@ def prefill_bench(torch, pkg, ops, synth, layers, layers_c, dev):
                       ids.data_ptr(), w.data_ptr(), K_TOP, o.data_ptr(), buf.data_ptr(),
                       buf.numel(), ops._stream())
 
-    us = timed(torch, run, 50, warmup=5)
+    us = timed(torch, run, iters, warmup=warmup)
     ws.check()
     flops = (T * K_TOP + T) * 2 * (H * 2 * I + I * H)
     counts = torch.bincount(ids.reshape(-1).long(), minlength=E)
     active = int((counts > 0).sum())
     wbytes = active * EXPERT_B + EXPERT_B
     tf = flops / us / 1e6
-    out["config2_T2048"] = {"us": round(us, 2), "tok_s": round(T / us * 1e6, 1),
-                            "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                            "hbm_weight_gbs": round(wbytes / us / 1e3, 1),
-                            "active_experts": active, "max_group": int(counts.max()),
-                            "flops": flops}
+    res = {"us": round(us, 2), "tok_s": round(T / us * 1e6, 1),
+           "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+           "hbm_weight_gbs": round(wbytes / us / 1e3, 1),
+           "active_experts": active, "max_group": int(counts.max()),
+           "flops": flops}
     log(f"prefill T=2048: {us:.1f} us, {T / us * 1e6:.0f} tok/s, {tf:.1f} TFLOP/s")
+    return res
+
+
+def prefill_bench(torch, pkg, ops, synth, layers, layers_c, dev):
+    out = {"config2_T2048": prefill_config2(torch, pkg, ops, synth, layers[0], layers_c, dev)}
     # config 4b: 40 layers, T=16384
     T = 16384
     x = synth.activations(T, H, 43, dev)
