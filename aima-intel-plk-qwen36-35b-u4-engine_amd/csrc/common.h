@@ -227,6 +227,55 @@ __device__ __forceinline__ float block_sum_256(float v, float* red) {
   return t;
 }
 
+// Row helpers for 256-thread blocks over an f16 row of H elements (H a
+// multiple of 8, row 16-byte aligned): thread i handles the 8-element chunks
+// i, i + 256, ... with 16-byte accesses.  Every caller of a helper sums in
+// the same order, so fused and standalone uses agree bit for bit.
+__device__ __forceinline__ float row_dot_f16(const uint16_t* __restrict__ a,
+                                             const uint16_t* __restrict__ b, int64_t H,
+                                             float* red) {
+  float s = 0.f;
+  for (int64_t i = threadIdx.x * 8; i < H; i += 2048) {
+    const u32x4 va = *reinterpret_cast<const u32x4*>(a + i);
+    const u32x4 vb = *reinterpret_cast<const u32x4*>(b + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s += h2f((uint16_t)(va[j] & 0xffffu)) * h2f((uint16_t)(vb[j] & 0xffffu));
+      s += h2f((uint16_t)(va[j] >> 16)) * h2f((uint16_t)(vb[j] >> 16));
+    }
+  }
+  return block_sum_256(s, red);
+}
+
+// out = f16(x * (1 / sqrt(mean(x^2) + eps)) * w)
+__device__ __forceinline__ void rmsnorm_row(const uint16_t* __restrict__ x,
+                                            const float* __restrict__ w, int64_t H, float eps,
+                                            uint16_t* __restrict__ out, float* red) {
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x * 8; i < H; i += 2048) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(x + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = h2f((uint16_t)(v[j] & 0xffffu)), hi = h2f((uint16_t)(v[j] >> 16));
+      ss += lo * lo;
+      ss += hi * hi;
+    }
+  }
+  ss = block_sum_256(ss, red);
+  const float scale = 1.0f / sqrtf(ss / (float)H + eps);
+  for (int64_t i = threadIdx.x * 8; i < H; i += 2048) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(x + i);
+    u32x4 o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = h2f((uint16_t)(v[j] & 0xffffu)) * scale * w[i + 2 * j];
+      const float hi = h2f((uint16_t)(v[j] >> 16)) * scale * w[i + 2 * j + 1];
+      o[j] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+    }
+    *reinterpret_cast<u32x4*>(out + i) = o;
+  }
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float s = g >= 0.f ? 1.f / (1.f + expf(-g)) : expf(g) / (1.f + expf(g));
   return g * s * u;

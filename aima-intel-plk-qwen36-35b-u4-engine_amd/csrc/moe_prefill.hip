@@ -49,6 +49,7 @@ struct PrefillWs {
   uint16_t* contrib;     // [A + T][H] f16
   uint16_t* h;           // [T][H]   (stack only)
   uint16_t* r[2];        // [T][H]   (stack only)
+  float* sigma[2];       // [T]      (stack only: shared-expert gates, by layer parity)
 };
 
 struct PrefillDims {
@@ -99,6 +100,8 @@ static size_t prefill_ws_layout(const PrefillDims& d, WsMode mode, void* base, P
     l.h = reinterpret_cast<uint16_t*>(take((size_t)d.T * d.H * 2));
     l.r[0] = reinterpret_cast<uint16_t*>(take((size_t)d.T * d.H * 2));
     l.r[1] = reinterpret_cast<uint16_t*>(take((size_t)d.T * d.H * 2));
+    l.sigma[0] = reinterpret_cast<float*>(take((size_t)d.T * 4));
+    l.sigma[1] = reinterpret_cast<float*>(take((size_t)d.T * 4));
   }
   if (w) *w = l;
   return off;
@@ -244,12 +247,12 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
   const int b0 = pidx * chunk, b1 = min(nb, b0 + chunk);
   int sum = 0;
   if (e < E) {
-    for (int b = b0; b < b1; b += 8) {
-      int c[8];
+    for (int b = b0; b < b1; b += 16) {
+      int c[16];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) c[j] = b + j < b1 ? block_base[(int64_t)(b + j) * E + e] : 0;
+      for (int j = 0; j < 16; ++j) c[j] = b + j < b1 ? block_base[(int64_t)(b + j) * E + e] : 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) sum += c[j];
+      for (int j = 0; j < 16; ++j) sum += c[j];
     }
   }
   part[tid] = sum;
@@ -275,12 +278,12 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
   __syncthreads();
   if (e < E) {
     int run = part[e] + before;
-    for (int b = b0; b < b1; b += 8) {
-      int c[8];
+    for (int b = b0; b < b1; b += 16) {
+      int c[16];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) c[j] = b + j < b1 ? block_base[(int64_t)(b + j) * E + e] : 0;
+      for (int j = 0; j < 16; ++j) c[j] = b + j < b1 ? block_base[(int64_t)(b + j) * E + e] : 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < 16; ++j) {
         if (b + j < b1) block_base[(int64_t)(b + j) * E + e] = run;
         run += c[j];
       }
@@ -702,18 +705,37 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
 // ---------------------------------------------------------------------------
 // combine: out[t] = f16(residual[t] + (sum_r contrib[inv[t][r]] + sigma_t * shared[t]))
 // ---------------------------------------------------------------------------
+// sigma_t = sigmoid(gate_vec . x[t]) in f64, the dot in row_dot_f16's
+// order for every caller (so a precomputed value is bit-identical).
+__device__ __forceinline__ float shared_gate_sigma(const uint16_t* __restrict__ gate_vec,
+                                                   const uint16_t* __restrict__ xr, int64_t H,
+                                                   float* red) {
+  const double gd = row_dot_f16(gate_vec, xr, H, red);
+  return (float)(gd >= 0.0 ? 1.0 / (1.0 + exp(-gd)) : exp(gd) / (1.0 + exp(gd)));
+}
+
+// Layer stacks also fuse the next layer's input: with next_norm set, the
+// block RMS-normalizes the row it just wrote (rmsnorm_row, the rmsnorm
+// kernel's arithmetic and summation order) into next_h, and computes that layer's
+// shared-expert gate into next_sigma, which the next combine reads as
+// sigma_in instead of re-reading its input.
+struct CombineNext {
+  const float* norm;          // next layer's RMSNorm weight (null: no fusion)
+  const uint16_t* gate_vec;   // next layer's shared gate vector
+  float eps;
+  uint16_t* h;                // [T][H] next layer's normalized input
+  float* sigma;               // [T]
+};
+
 __global__ __launch_bounds__(256) void combine_kernel(
     const uint16_t* __restrict__ contrib, const int32_t* __restrict__ inverse_map, int k,
     int64_t A, const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate_vec,
-    const uint16_t* __restrict__ residual, int64_t H, uint16_t* __restrict__ out) {
+    const float* __restrict__ sigma_in, const uint16_t* __restrict__ residual, int64_t H,
+    uint16_t* __restrict__ out, CombineNext next) {
   __shared__ float red[4];
   __shared__ int rowsel[16];
   const int64_t t = blockIdx.x;
-  float g = 0.f;
-  for (int64_t i = threadIdx.x; i < H; i += 256) g += h2f(gate_vec[i]) * h2f(x[t * H + i]);
-  g = block_sum_256(g, red);
-  const double gd = g;
-  const float sigma = (float)(gd >= 0.0 ? 1.0 / (1.0 + exp(-gd)) : exp(gd) / (1.0 + exp(gd)));
+  const float sigma = sigma_in ? sigma_in[t] : shared_gate_sigma(gate_vec, x + t * H, H, red);
   if (threadIdx.x < k) rowsel[threadIdx.x] = inverse_map[t * k + threadIdx.x];
   __syncthreads();
   const uint16_t* shared_row = contrib + (A + t) * H;
@@ -750,6 +772,13 @@ __global__ __launch_bounds__(256) void combine_kernel(
     for (int j = 0; j < 4; ++j) ov[j] = (uint32_t)f2h(o[2 * j]) | ((uint32_t)f2h(o[2 * j + 1]) << 16);
     *reinterpret_cast<u32x4*>(out + t * H + h) = ov;
   }
+  if (next.norm) {
+    __syncthreads();  // the row is complete (rmsnorm_row reads it back)
+    rmsnorm_row(out + t * H, next.norm, H, next.eps, next.h + t * H, red);
+    __syncthreads();
+    const float sn = shared_gate_sigma(next.gate_vec, next.h + t * H, H, red);
+    if (threadIdx.x == 0) next.sigma[t] = sn;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -780,9 +809,12 @@ static int launch_schedule(const int32_t* ids, const float* weights, const Prefi
   return launch_check("grouped schedule scatter");
 }
 
+// sigma_in: the shared-expert gate per token if already known (null: the
+// combine computes it from x); next: fusion of the next layer's input.
 static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint16_t* residual,
                          const int32_t* ids, const float* weights, uint16_t* out,
-                         const PrefillDims& d, const PrefillWs& w, hipStream_t st) {
+                         const PrefillDims& d, const PrefillWs& w, hipStream_t st,
+                         const float* sigma_in = nullptr, CombineNext next = CombineNext{}) {
   int rc = launch_schedule(ids, weights, d, w, st);
   if (rc != AIMA_OK) return rc;
   const unsigned mtiles = (unsigned)round_up(d.max_tiles, 8);
@@ -803,7 +835,8 @@ static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint1
   rc = launch_check("grouped down GEMM");
   if (rc != AIMA_OK) return rc;
   hipLaunchKernelGGL(combine_kernel, dim3((unsigned)d.T), dim3(256), 0, st, w.contrib,
-                     w.inverse_map, d.k, d.A, x, L.shared_gate_vec, residual, (int64_t)d.H, out);
+                     w.inverse_map, d.k, d.A, x, L.shared_gate_vec, sigma_in, residual,
+                     (int64_t)d.H, out, next);
   return launch_check("grouped combine");
 }
 
@@ -831,8 +864,9 @@ int check_layer_prefill(const aima_moe_layer* L, int k, bool need_norm) {
     return fail(AIMA_E_UNSUPPORTED, "moe prefill: hidden % 256 and inter % 128 must be 0");
   }
   AIMA_REQUIRE(aligned(L->gate_up.qweight, 16) && aligned(L->down.qweight, 16) &&
-                   aligned(L->shared_gate_up.qweight, 16) && aligned(L->shared_down.qweight, 16),
-               "moe prefill: qweight pointers must be 16-byte aligned");
+                   aligned(L->shared_gate_up.qweight, 16) && aligned(L->shared_down.qweight, 16) &&
+                   aligned(L->shared_gate_vec, 16),
+               "moe prefill: qweight pointers and the shared gate vector must be 16-byte aligned");
   return AIMA_OK;
 }
 
@@ -871,7 +905,8 @@ extern "C" int aima_moe_grouped_prefill(const aima_moe_layer* layer, const uint1
   AIMA_REQUIRE(prefill_offsets_fit(layer, tokens, k),
                "moe_grouped_prefill: tokens * (k + 1) * inter and tokens * hidden must stay below "
                "2^30 (split the batch)");
-  AIMA_REQUIRE(aligned(x, 16), "moe_grouped_prefill: x must be 16-byte aligned");
+  AIMA_REQUIRE(aligned(x, 16) && aligned(out, 16) && (!residual || aligned(residual, 16)),
+               "moe_grouped_prefill: x, residual and out must be 16-byte aligned");
   const PrefillDims d = prefill_dims(layer, tokens, k);
   PrefillWs w{};
   const size_t need = prefill_ws_layout(d, WsMode::kLayer, workspace, &w);
@@ -888,6 +923,8 @@ extern "C" int aima_moe_stack_prefill(const aima_moe_layer* layers, int32_t n_la
                                       void* workspace, size_t workspace_bytes, void* stream) {
   AIMA_REQUIRE(layers && n_layers > 0, "moe_stack_prefill: need at least one layer");
   AIMA_REQUIRE(x_in && ids && weights && out, "moe_stack_prefill: null pointer");
+  AIMA_REQUIRE(aligned(x_in, 16) && aligned(out, 16),
+               "moe_stack_prefill: x and out must be 16-byte aligned");
   AIMA_REQUIRE(tokens > 0 && tokens <= (1 << 24), "moe_stack_prefill: tokens must be in [1, 2^24]");
   AIMA_REQUIRE(prefill_offsets_fit(layers, tokens, k),
                "moe_stack_prefill: tokens * (k + 1) * inter and tokens * hidden must stay below "
@@ -908,13 +945,23 @@ extern "C" int aima_moe_stack_prefill(const aima_moe_layer* layers, int32_t n_la
   AIMA_REQUIRE(aligned(workspace, 256), "moe_stack_prefill: workspace must be 256-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   const uint16_t* r = x_in;
+  // layer 0's normalized input comes from the rmsnorm kernel; every later
+  // one (and its shared-expert gate) from the previous layer's combine
+  int rc = rmsnorm_launch(r, layers[0].norm_weight, tokens, layers[0].hidden, eps, w.h, st);
+  if (rc != AIMA_OK) return rc;
   for (int32_t l = 0; l < n_layers; ++l) {
     const aima_moe_layer& L = layers[l];
-    int rc = rmsnorm_launch(r, L.norm_weight, tokens, L.hidden, eps, w.h, st);
-    if (rc != AIMA_OK) return rc;
     uint16_t* dst = (l == n_layers - 1) ? out : w.r[l & 1];
+    CombineNext next{};
+    if (l + 1 < n_layers) {
+      next.norm = layers[l + 1].norm_weight;
+      next.gate_vec = layers[l + 1].shared_gate_vec;
+      next.eps = eps;
+      next.h = w.h;  // each block rewrites only its own row, after reading it
+      next.sigma = w.sigma[(l + 1) & 1];
+    }
     rc = prefill_layer(L, w.h, r, ids + (int64_t)l * d.A, weights + (int64_t)l * d.A, dst, d, w,
-                       st);
+                       st, l > 0 ? w.sigma[l & 1] : nullptr, next);
     if (rc != AIMA_OK) return rc;
     r = dst;
   }

@@ -145,21 +145,13 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
                                                       uint16_t* __restrict__ out) {
   __shared__ float red[4];
   const int64_t row = blockIdx.x;
-  const uint16_t* xr = x + row * hidden;
-  float ss = 0.f;
-  for (int64_t i = threadIdx.x; i < hidden; i += 256) {
-    const float v = h2f(xr[i]);
-    ss += v * v;
-  }
-  ss = block_sum_256(ss, red);
-  const float scale = 1.0f / sqrtf(ss / (float)hidden + eps);
-  for (int64_t i = threadIdx.x; i < hidden; i += 256) {
-    out[row * hidden + i] = f2h(h2f(xr[i]) * scale * weight[i]);
-  }
+  rmsnorm_row(x + row * hidden, weight, hidden, eps, out + row * hidden, red);
 }
 
 int rmsnorm_launch(const uint16_t* x, const float* weight, int64_t rows, int64_t hidden,
                    float eps, uint16_t* out, hipStream_t st) {
+  AIMA_REQUIRE(hidden % 8 == 0 && aligned(x, 16) && aligned(out, 16),
+               "rmsnorm: hidden must be a multiple of 8 and x, out 16-byte aligned");
   hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, st, x, weight, hidden,
                      eps, out);
   return launch_check("rmsnorm");
