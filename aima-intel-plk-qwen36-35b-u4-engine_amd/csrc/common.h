@@ -74,6 +74,12 @@ __device__ __forceinline__ float h2f(uint16_t b) {
 __device__ __forceinline__ uint16_t f2h(float f) {
   return __builtin_bit_cast(uint16_t, (_Float16)f);
 }
+// Two floats -> f16x2 bits (lo in bits 0..15), round to nearest even: one
+// v_cvt_pk_f16_f32 on gfx950.
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), f16x2));
+}
 
 __device__ __forceinline__ uint32_t u4_code(const uint8_t* packed, int64_t i) {
   const uint32_t b = packed[i >> 1];
@@ -270,7 +276,7 @@ __device__ __forceinline__ void rmsnorm_row(const uint16_t* __restrict__ x,
     for (int j = 0; j < 4; ++j) {
       const float lo = h2f((uint16_t)(v[j] & 0xffffu)) * scale * w[i + 2 * j];
       const float hi = h2f((uint16_t)(v[j] >> 16)) * scale * w[i + 2 * j + 1];
-      o[j] = (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+      o[j] = pack_h2(lo, hi);
     }
     *reinterpret_cast<u32x4*>(out + i) = o;
   }

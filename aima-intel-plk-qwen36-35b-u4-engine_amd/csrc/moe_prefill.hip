@@ -10,9 +10,10 @@
 // 2. Grouped gate/up GEMM (MFMA v_mfma_f32_32x32x16_f16): per tile, the token
 //    rows are gathered into LDS; each wave dequantizes its own 32 weight rows
 //    straight into MFMA operands as f16 (q - z) * s and multiplies them with
-//    every token row of the tile.  The SwiGLU epilogue writes f16 [rows][I].
-// 3. Grouped down GEMM, same structure over K = I; the epilogue multiplies by
-//    the router weight and writes f16 contributions [rows][H].
+//    every token row of the tile.  The SwiGLU epilogue scales each row by its
+//    router weight (1 for the shared expert) and writes f16 [rows][I].
+// 3. Grouped down GEMM, same structure over K = I; its output rows are then
+//    the weighted contributions, written as f16 [rows][H].
 // 4. Combine: per token, the k contributions in rank order, plus the
 //    sigmoid-gated shared row, plus the residual, summed in f32 and rounded
 //    to f16.
@@ -368,7 +369,7 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d, f16x2 zz2, f16x2 ss2, uint
   return __builtin_bit_cast(f16x8, v);
 }
 
-// Direct global -> LDS loads (each lane's 16 bytes land at the
+// Direct global -> LDS loads (each lane's 16 or 4 bytes land at the
 // wave-uniform LDS address + lane * size), addressed as a wave-uniform base
 // (SGPRs) plus a 32-bit per-lane byte offset.  Issued through inline
 // assembly: the compiler then neither counts them nor orders LDS reads behind
@@ -386,6 +387,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* lds) {
 // `lds` is the wave-uniform LDS byte address (see lds_addr).
 __device__ __forceinline__ void lds_load16(const void* base, uint32_t off, uint32_t lds) {
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(lds)
+               : "memory");
+}
+__device__ __forceinline__ void lds_load4(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "{m0}"(lds)
                : "memory");
 }
 // Block barrier that does not wait for outstanding memory operations (the
@@ -425,6 +430,7 @@ __device__ __forceinline__ void plain_barrier() {
 constexpr int kGemmThreads = 512;
 constexpr int kStageA = kBM * 128 * 2;   // token rows of one group, bytes
 constexpr int kSmemBytes = 2 * kStageA;  // two-buffer ring; the epilogue reuses it
+constexpr int kSmemWeights = kSmemBytes;  // gate/up: router weights of the tile rows (1 KB)
 
 struct GemmTile {
   const void* a_base;     // token rows (uniform)
@@ -482,6 +488,15 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
   const uint32_t magic = u4_magic();
+
+  // gate/up: the tile rows' router weights go to LDS with the first loads
+  // (waves 0-3, one row per lane; rows past the tile read the first row)
+  const bool routed = t.e < t.E;
+  if (GATEUP && routed && wave < kBM / 64) {
+    const int r = wave * 64 + lane;
+    lds_load4(uniform_ptr(row_weight), (uint32_t)((t.row0 + (r < t.rows ? r : 0)) * 4),
+              lds0 + (uint32_t)(kSmemWeights + wave * 256));
+  }
 
   // sA: the group's token rows in LDS, row m at sA + 256 m
   auto compute = [&](int g, const uint8_t* sA, const WGroup& w) {
@@ -573,12 +588,12 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
   const int64_t H = L.hidden, I = L.inter;
   constexpr int kChunks = GATEUP ? 16 : 32;   // 16-byte chunks per tile row
   constexpr int kRowBytes = kChunks * 16;
+  // gate/up scales the activations by the router weight (the down
+  // projection is linear, so its output is the weighted contribution)
   float wt[MB];
+  const float* s_wt = reinterpret_cast<const float*>(smem + kSmemWeights);
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int m = mb * 32 + n;
-    wt[mb] = (!GATEUP && t.e < t.E && m < t.rows) ? row_weight[t.row0 + m] : 1.0f;
-  }
+  for (int mb = 0; mb < MB; ++mb) wt[mb] = (GATEUP && routed) ? s_wt[mb * 32 + n] : 1.0f;
   __syncthreads();  // every wave is done with the token-row buffers
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
@@ -588,10 +603,10 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         u32x2 v;
-        v.x = (uint32_t)f2h(silu_mul_fast(acc[mb][4 * q + 0], acc[mb][8 + 4 * q + 0])) |
-              ((uint32_t)f2h(silu_mul_fast(acc[mb][4 * q + 1], acc[mb][8 + 4 * q + 1])) << 16);
-        v.y = (uint32_t)f2h(silu_mul_fast(acc[mb][4 * q + 2], acc[mb][8 + 4 * q + 2])) |
-              ((uint32_t)f2h(silu_mul_fast(acc[mb][4 * q + 3], acc[mb][8 + 4 * q + 3])) << 16);
+        v.x = pack_h2(wt[mb] * silu_mul_fast(acc[mb][4 * q + 0], acc[mb][8 + 4 * q + 0]),
+                      wt[mb] * silu_mul_fast(acc[mb][4 * q + 1], acc[mb][8 + 4 * q + 1]));
+        v.y = pack_h2(wt[mb] * silu_mul_fast(acc[mb][4 * q + 2], acc[mb][8 + 4 * q + 2]),
+                      wt[mb] * silu_mul_fast(acc[mb][4 * q + 3], acc[mb][8 + 4 * q + 3]));
         const int chunk = (wave * 2 + q) ^ (m & (kChunks - 1));
         *reinterpret_cast<u32x2*>(rowp + chunk * 16 + hh * 8) = v;
       }
@@ -599,10 +614,8 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         u32x2 v;
-        v.x = (uint32_t)f2h(wt[mb] * acc[mb][4 * q + 0]) |
-              ((uint32_t)f2h(wt[mb] * acc[mb][4 * q + 1]) << 16);
-        v.y = (uint32_t)f2h(wt[mb] * acc[mb][4 * q + 2]) |
-              ((uint32_t)f2h(wt[mb] * acc[mb][4 * q + 3]) << 16);
+        v.x = pack_h2(acc[mb][4 * q + 0], acc[mb][4 * q + 1]);
+        v.y = pack_h2(acc[mb][4 * q + 2], acc[mb][4 * q + 3]);
         const int chunk = (wave * 4 + q) ^ (m & (kChunks - 1));
         *reinterpret_cast<u32x2*>(rowp + chunk * 16 + hh * 8) = v;
       }
@@ -633,7 +646,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
     const int32_t* __restrict__ tile_count, const int32_t* __restrict__ token_map,
     const float* __restrict__ row_weight, int64_t A, int ntiles_n,
     uint16_t* __restrict__ act_out, uint16_t* __restrict__ contrib_out) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes + kBM * 4];
   const int p = blockIdx.x;
   const int slot = p >> 3;
   const int mt = (slot / ntiles_n) * 8 + (p & 7);
@@ -769,7 +782,7 @@ __global__ __launch_bounds__(256) void combine_kernel(
     }
     u32x4 ov;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) ov[j] = (uint32_t)f2h(o[2 * j]) | ((uint32_t)f2h(o[2 * j + 1]) << 16);
+    for (int j = 0; j < 4; ++j) ov[j] = pack_h2(o[2 * j], o[2 * j + 1]);
     *reinterpret_cast<u32x4*>(out + t * H + h) = ov;
   }
   if (next.norm) {
