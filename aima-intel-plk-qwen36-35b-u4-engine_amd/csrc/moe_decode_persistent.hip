@@ -1,37 +1,48 @@
 // Persistent batch-1 decode of an MoE FFN stack (all layers in one launch).
 //
-// Launch: one 512-thread block per CU, cooperative (every block resident).
-// Wave 0 of each block is the control wave; waves 1..7 compute.
+// Launch: 256 blocks of 512 threads, one per CU, cooperative (all resident).
+// MI355X has 8 XCDs of 32 CUs, each XCD with its own L2; blocks are placed
+// on the XCDs round-robin.  A block reads its XCD id (x) from the hardware
+// and takes rank j = blockIdx / 8 inside it.  The work of a layer is split
+// by XCD so that only one exchange per layer crosses XCDs:
+//   XCD x owns routed slot x (the rank-x expert of the top-k) and slice x of
+//   the shared expert (its intermediate units 64x .. 64x+63).
+//   A_L  block (x, j) computes 18 of the XCD's 576 gate/up pairs (SwiGLU)
+//        and publishes them to its XCD (act_L, XCD-local).
+//   B_L  block (x, j) computes output rows 64j .. 64j+63 of
+//        P_x = c_x * down_x(act_x) + sigma * shared_down[:, slice x](act_sh,x)
+//        and publishes them to every XCD (cross-XCD).
+//   relay  block (x, j) sums P_0..P_7 for its 64 rows, adds the residual
+//        and publishes r_{L+1} rows to its XCD (XCD-local); every block of
+//        the XCD then reads all 2048 rows of r_{L+1}.
+// XCD-local words are written with plain stores, which stay in the XCD's
+// L2, and read with device-scope loads, which hit there (about 0.3 us one
+// way against 0.45 us for a device-scope store/load pair across XCDs,
+// measured on MI355X); cross-XCD words use device-scope stores and loads.
+// Each XCD-local buffer is indexed by the hardware XCD id, so only the CUs
+// of that XCD ever write or read it.
 //
-// Per layer L the work is the same as the two-launch decode (moe_decode.hip):
-//   A_L  rows of the k routed + shared gate/up matrices -> SwiGLU -> act_L
-//   B_L  rows of the down matrices, weighted sum, residual -> r_{L+1}
-// but no launch or grid barrier separates the phases.  Every value another
-// block consumes is published as a self-validating word: {f16 value, u16
-// epoch} for the residual, {3 x f16, u16 epoch} records (64-bit, written
-// atomically) for the activations, {id, epoch} / {f32, epoch} for the routes.
-// A consumer polls the words it needs with device-coherent loads until every
-// epoch matches the one expected for this launch and phase, so the wait and
-// the data transfer are one round trip.
-// Ordering argument: a block can only publish act_{L+1} after seeing all of
-// r_{L+1}, i.e. after every block finished B_L (and thus its reads of act_L),
-// and likewise for r; with buffers alternating by layer parity a word can
-// never be overwritten while a reader still expects it.  Epochs are unique
-// per launch, so stale words left by an earlier launch never match: every
-// block reads the launch counter when it starts and block 0 advances it when
-// it exits, which cannot happen before every block has started (block 0's
-// last phase consumes an output of every block).
-//
-// Everything a block needs that does not depend on other blocks' results of
-// the current layer is fetched ahead: all routes once at the start, the next
-// layer's norm weight and shared-expert gate vector into LDS during B_L, and
-// each wave's weight rows for the next phase right after the previous one.
-// So each phase boundary costs only the exchange itself.  The control wave
-// turns r_L into the A-phase operands (RMSNorm, per-chunk pairs and sums, the
-// shared-expert gate sigmoid, computed by every block for itself) and stages
-// act_L; the compute waves build their own B-phase chunk operands.  Every
-// poll has a spin limit: on expiry the block records AIMA_DEVERR_TIMEOUT and
-// all its waves return, so no wave can wait forever.
+// Every value another block consumes is a self-validating word: {f16 value,
+// u16 epoch} for the residual, {3 x f16, u16 epoch} 64-bit records for the
+// activations, {f32, u32 epoch} for the partial outputs P, {id, epoch} /
+// {f32, epoch} for the routes.  A consumer polls until every epoch matches
+// the one expected for this launch and phase, so the wait and the transfer
+// are one round trip.  Buffers alternate by layer parity, and a buffer is
+// rewritten two layers later only after every reader finished with it:
+// act_{L+2} is published after reading r_{L+2}, which needs P_{L+1} of every
+// block, each published after its XCD's act_{L+1} was complete, i.e. after
+// every block had finished B_L (its reads of act_L).  P_{L+2} needs act_{L+2}
+// of the XCD, hence r_{L+2}, hence the XCD's relays of layer L+1, which read
+// P_{L+1} of every block; each block published P_{L+1} after reading r_{L+1},
+// i.e. after all relays of its XCD had consumed P_L.  r_{L+3} is published by
+// a relay after reading P_{L+2} of its own block, i.e. after every block of
+// the XCD had read r_{L+2} (and so finished with r_{L+1}).  Epochs are unique
+// per launch: every block reads the launch counter when it starts, and block
+// 0 advances it on exit, which happens only after every block has published
+// (block 0's last residual read depends on P of every block; with one layer
+// block 0 waits for all P words explicitly).
+// Every poll has a spin limit: on expiry the block records
+// AIMA_DEVERR_TIMEOUT and all its waves return.
 #include "common.h"
 
 #include <math.h>
@@ -42,21 +53,31 @@ namespace aima {
 
 namespace {
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 constexpr int kThreads = 512;
-constexpr int kComputeWaves = 7;
-constexpr int kH = 2048;             // hidden (specialization)
-constexpr int kI = 512;              // expert intermediate (specialization)
-constexpr int kMaxRowsA = 6;         // gate/up rows per compute wave
-constexpr int kMaxUnitsB = 3;        // (slot, 4-row pass) units per compute wave
+constexpr int kWaves = kThreads / 64;
+constexpr int kH = 2048;                                 // hidden (specialization)
+constexpr int kI = 512;                                  // expert intermediate (specialization)
+constexpr int kXcds = 8;
+constexpr int kPerXcd = 32;                              // blocks per XCD
+constexpr int kBlocks = kXcds * kPerXcd;                 // 256
+constexpr int kSlice = kI / kXcds;                       // shared-expert units per XCD
+constexpr int kXcdPairs = kI + kSlice;                   // 576 gate/up pairs per XCD
+constexpr int kPairs = kXcdPairs / kPerXcd;              // 18 pairs per block
+constexpr int kRowsA = 2 * kPairs;                       // 36 gate/up rows per block
+constexpr int kMaxRowsA = (kRowsA + kWaves - 1) / kWaves;  // 5 rows per wave at most
+constexpr int kRowsB = kH / kPerXcd;                     // 64 output rows per block
+constexpr int kWaveRowsB = kRowsB / kWaves;              // 8 output rows per wave
+constexpr int kActRecords = kXcdPairs / 3;               // 192 act records per XCD
+constexpr int kActStride = 256;                          // records per (XCD, parity) buffer
+constexpr int kChunksA = kH / 32;                        // A-phase operand chunks
+constexpr int kChunksB = kXcdPairs / 32;                 // 18 B-phase operand chunks
 constexpr int kMaxK = 8;
-constexpr int kMaxSlots = kMaxK + 1;
-constexpr int kRowsB = 8;            // output rows per block
 constexpr uint32_t kSpinLimit = 1u << 22;
 constexpr int kMaxLayers = 79;
-constexpr int kChunksA = kH / 32;                   // A-phase operand chunks
-constexpr int kChunksB = kMaxUnitsB * (kI / 32);    // B-phase chunks per wave
-constexpr int kActRecords = kMaxSlots * kI / 3;     // act records per parity buffer
-constexpr int kAuxCoherent = 16;                    // sc1: device-coherent load
+static_assert(kPairs % 3 == 0, "blocks own whole act records");
+static_assert(kRowsB % kWaves == 0 && kWaveRowsB == 8, "8 output rows per wave");
 
 struct PersistArgs {
   const aima_moe_layer* layers;   // device table [n_layers]
@@ -71,10 +92,11 @@ struct PersistArgs {
   float eps;
   const uint16_t* r0;             // f16 [H]
   uint16_t* out;                  // f16 [H]
-  uint32_t* r_buf;                // [2][H]            {f16, epoch}, chunk-interleaved
-  uint64_t* act_buf;              // [2][kActRecords]  {3 x f16, epoch}
-  uint32_t* route_ids;            // [L][k]            {id, epoch}
-  uint64_t* route_w;              // [L][k]            {f32, epoch}
+  uint32_t* rx;                   // [xcd][2][H]            {f16, epoch}, XCD-local
+  uint64_t* actx;                 // [xcd][2][kActStride]   {3 x f16, epoch}, XCD-local
+  uint64_t* pbuf;                 // [2][H][xcd]            {f32, epoch}
+  uint32_t* route_ids;            // [L][k]                 {id, epoch}
+  uint64_t* route_w;              // [L][k]                 {f32, epoch}
   uint32_t* epoch_counter;
   uint32_t* err;
 };
@@ -91,6 +113,38 @@ __device__ __forceinline__ void st_coherent32(uint32_t* p, uint32_t v) {
 __device__ __forceinline__ void st_coherent64(uint64_t* p, uint64_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// XCD-local stores: plain global stores, which complete in the XCD's L2.
+__device__ __forceinline__ void st_local32(uint32_t* p, uint32_t v) {
+  asm volatile("global_store_dword %0, %1, off" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st_local64(uint64_t* p, uint64_t v) {
+  asm volatile("global_store_dwordx2 %0, %1, off" : : "v"(p), "v"(v) : "memory");
+}
+// Poll loads: device-scope (sc1) 16-byte loads issued together, then one
+// wait.  Written as asm so that repeated polls are never merged or hoisted
+// (a volatile buffer load would also set sc0, which measured slower).
+__device__ __forceinline__ u32x4 poll1(const void* p) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off sc1\n\ts_waitcnt vmcnt(0)"
+               : "=v"(v) : "v"(p) : "memory");
+  return v;
+}
+__device__ __forceinline__ void poll2(const void* p, const void* q, u32x4& v, u32x4& w) {
+  asm volatile(
+      "global_load_dwordx4 %0, %2, off sc1\n\t"
+      "global_load_dwordx4 %1, %3, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v), "=&v"(w) : "v"(p), "v"(q) : "memory");
+}
+__device__ __forceinline__ void poll4(const void* p, u32x4 (&v)[4]) {
+  asm volatile(
+      "global_load_dwordx4 %0, %4, off sc1\n\t"
+      "global_load_dwordx4 %1, %4, off offset:16 sc1\n\t"
+      "global_load_dwordx4 %2, %4, off offset:32 sc1\n\t"
+      "global_load_dwordx4 %3, %4, off offset:48 sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]) : "v"(p) : "memory");
+}
 
 __device__ __forceinline__ uint32_t pack_word(uint16_t v, uint32_t epoch) {
   return (uint32_t)v | (epoch << 16);
@@ -99,32 +153,18 @@ __device__ __forceinline__ uint64_t pack_f32(float v, uint32_t epoch) {
   return (uint64_t)__builtin_bit_cast(uint32_t, v) | ((uint64_t)epoch << 32);
 }
 
-// Residual words are stored chunk-interleaved: value h = 32 c + 4 q + j sits
-// at word 4 (64 q + c) + j, so the 16-byte load q of lane c returns values
-// 4q..4q+3 of chunk c and the eight loads of a lane are coalesced across the
-// wave.  Each word validates itself, so a wide load needs no atomicity
-// beyond the 32-bit word.
-__device__ __forceinline__ int r_pos(int h) {
-  return ((((h & 31) >> 2) * 64 + (h >> 5)) << 2) + (h & 3);
-}
-
 struct SharedState {
   u32x4 xa_p[4][kChunksA];             // A operands: chunk pairs, word-group major
   float xa_bias[kChunksA];
   float xa_xsum[kChunksA];
-  uint32_t xb[kMaxSlots * kI / 2];     // act_L, f16 pairs (slot-major)
-  u32x4 xb_p[kComputeWaves][4][kChunksB];  // per compute wave B operands
-  float xb_bias[kComputeWaves][kChunksB];
-  float xb_xsum[kComputeWaves][kChunksB];
-  // RMSNorm weight (f32) and shared gate vector (f16) of the current layer,
-  // and the normalized activation x (f16), each stored so that lane c's
-  // 16-byte read q returns part q of chunk c (conflict-free LDS reads)
-  u32x4 nw_p[8][kChunksA];
-  u32x4 gv_p[4][kChunksA];
-  u32x4 xw_p[4][kChunksA];
-  float rowsum[kComputeWaves * kMaxRowsA];
-  float part[kMaxSlots][kRowsB];
-  float rown[kRowsB];                  // this block's residual rows (f32 of f16)
+  u32x4 xb_p[4][kChunksB];             // B operands (16 routed + 2 shared chunks)
+  float xb_bias[kChunksB];
+  float xb_xsum[kChunksB];
+  alignas(16) uint32_t act[kXcdPairs / 2];  // act_L of this XCD, f16 pairs
+  alignas(16) uint32_t rl[kH / 2];      // r_L, f16 pairs (read by the relay)
+  float ss[kWaves];                    // per-wave sums of squares of r_L
+  float gp[kWaves];                    // per-wave shared-gate partial dots
+  float rowsum[kRowsA];
   aima_moe_layer table[kMaxLayers];    // the layer table, copied once
   int32_t route_id[kMaxLayers][kMaxK];
   float route_w[kMaxLayers][kMaxK];
@@ -301,18 +341,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // wave-uniform values in scalar registers, so per-row branches and buffer
   // offsets below are scalar and never merge divergent loads
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int cw = wave - 1;  // compute wave index (valid for wave >= 1)
-  const int ct = threadIdx.x - 64;  // compute thread index (valid for wave >= 1)
   const int nb = gridDim.x;
   const int b = blockIdx.x;
   const int k = a.k;
-  const int slots = k + 1;
-  const int pairs = slots * kI;
-  // pairs per block, a multiple of 3 so each block owns whole act records
-  const int ppb = ((pairs + nb - 1) / nb + 2) / 3 * 3;
-  const int pair0 = b * ppb;
-  const int npairs = max(0, min(ppb, pairs - pair0));
-  const int h0 = b * kRowsB;
+  // hardware XCD id (HW_REG_XCC_ID bits 3:0) and the rank inside the XCD
+  const int x = (int)(__builtin_amdgcn_s_getreg((3 << 11) | 20) & 0xfu);
+  const int j = b >> 3;
   const uint32_t base = (*a.epoch_counter % 400u) * 160u + 1u;
   const uint32_t route_epoch = base + 2u * (uint32_t)a.n_layers;
   const int glog2 = a.group_log2;
@@ -331,7 +365,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     const int words = a.n_layers * (int)(sizeof(aima_moe_layer) / 4);
     for (int i = threadIdx.x; i < words; i += kThreads) dst[i] = src[i];
   }
-  if (threadIdx.x < kRowsB) S.rown[threadIdx.x] = h2f(a.r0[h0 + threadIdx.x]);
   // block 0 advances the launch counter on every exit path
   auto finish = [&]() {
     if (b == 0 && threadIdx.x == 0) *a.epoch_counter = *a.epoch_counter + 1u;
@@ -342,45 +375,15 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       S.abort = 1;
     }
   };
+  if (x >= kXcds || nb != kBlocks) {
+    // not on the 8 x 32 CU layout this kernel partitions for: every wait of
+    // the other blocks then expires and reports a timeout
+    if (threadIdx.x == 0) atomicOr(a.err, AIMA_DEVERR_TIMEOUT);
+    finish();
+    return;
+  }
   __syncthreads();
 
-  // norm weight (f32) and shared gate vector (f16) of a layer: 768 16-byte
-  // pieces, two per compute thread at most, staged through registers
-  auto load_vec = [&](int L, u32x4* v) {
-    const aima_moe_layer& Ly = S.table[L];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int c = ct + j * (kThreads - 64);
-      if (c < kH / 4) {
-        v[j] = gload16(Ly.norm_weight + 4 * c);
-      } else if (c < kH / 4 + kH / 8) {
-        v[j] = gload16(Ly.shared_gate_vec + 8 * (c - kH / 4));
-      }
-    }
-  };
-  auto store_vec = [&](const u32x4* v) {
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int c = ct + j * (kThreads - 64);
-      if (c < kH / 4) {
-        S.nw_p[c & 7][c >> 3] = v[j];            // floats 4c.. = chunk c/8, part c%8
-      } else if (c < kH / 4 + kH / 8) {
-        const int g = c - kH / 4;                // halves 8g.. = chunk g/4, part g%4
-        S.gv_p[g & 3][g >> 2] = v[j];
-      }
-    }
-  };
-  // route of layer L into LDS (ids range-checked); one wave, lanes < k
-  auto put_route = [&](int L, int id, float w) {
-    if (lane < k) {
-      if (id < 0 || id >= a.experts) {
-        atomicOr(a.err, AIMA_DEVERR_EXPERT_RANGE);
-        id = -1;
-      }
-      S.route_id[L][lane] = id;
-      S.route_w[L][lane] = w;
-    }
-  };
   auto local_route = [&](int L, int32_t* id, float* w) {
     if (a.logits) {
       route_layer(a.logits + (int64_t)L * a.experts, a.experts, k, a.min_weight_sum, id, w);
@@ -389,52 +392,60 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       *w = a.w_in[L * k + lane];
     }
   };
-  // poll the route block L published (returns false on timeout)
-  auto poll_route = [&](int L) -> bool {
+  // ---- prologue --------------------------------------------------------------
+  // Block L computes and publishes layer L's route (wave 0); then every block
+  // reads all routes into LDS (one wave per layer, in parallel).
+  if (wave == 0) {
+    for (int L = b; L < a.n_layers; L += nb) {
+      int32_t id = 0;
+      float w = 0.f;
+      local_route(L, &id, &w);
+      if (lane < k) {
+        if (id < 0 || id >= a.experts) id = 0xffff;  // flagged when read
+        st_coherent32(&a.route_ids[L * k + lane], pack_word((uint16_t)id, route_epoch));
+        st_coherent64(&a.route_w[L * k + lane], pack_f32(w, route_epoch));
+      }
+    }
+  }
+  // lane l of wave w reads slot l & 7 of layer L0 + w + 8 (l >> 3)
+  for (int L0 = 0; L0 < a.n_layers; L0 += 8 * kWaves) {
+    const int L = L0 + wave + kWaves * (lane >> 3);
+    const int s = lane & 7;
+    const bool mine = L < a.n_layers && s < k;
     uint32_t spins = 0;
     while (true) {
       bool ok = true;
       uint32_t idw = 0;
       uint64_t ww = 0;
-      if (lane < k) {
-        idw = ld_coherent32(&a.route_ids[L * k + lane]);
-        ww = ld_coherent64(&a.route_w[L * k + lane]);
+      if (mine) {
+        idw = ld_coherent32(&a.route_ids[L * k + s]);
+        ww = ld_coherent64(&a.route_w[L * k + s]);
         ok = (idw >> 16) == route_epoch && (uint32_t)(ww >> 32) == route_epoch;
       }
       if (__all(ok)) {
-        put_route(L, (int)(idw & 0xffffu), __builtin_bit_cast(float, (uint32_t)ww));
-        return true;
-      }
-      if (++spins > kSpinLimit) return false;
-      __builtin_amdgcn_s_sleep(2);
-    }
-  };
-
-  // ---- prologue --------------------------------------------------------------
-  // Every block computes layer 0's route itself (wave 0); block L >= 1
-  // publishes layer L's route (wave 2), which is polled one layer ahead.
-  if (wave == 0) {
-    int32_t id = 0;
-    float w = 0.f;
-    local_route(0, &id, &w);
-    put_route(0, id, w);
-  } else {
-    u32x4 v[2];
-    load_vec(0, v);
-    store_vec(v);
-    if (wave == 2) {
-      for (int L = (b == 0 ? nb : b); L < a.n_layers; L += nb) {
-        int32_t id = 0;
-        float w = 0.f;
-        local_route(L, &id, &w);
-        if (lane < k) {
-          st_coherent32(&a.route_ids[L * k + lane], pack_word((uint16_t)id, route_epoch));
-          st_coherent64(&a.route_w[L * k + lane], pack_f32(w, route_epoch));
+        if (mine) {
+          int id = (int)(idw & 0xffffu);
+          if (id >= a.experts) {
+            atomicOr(a.err, AIMA_DEVERR_EXPERT_RANGE);
+            id = -1;
+          }
+          S.route_id[L][s] = id;
+          S.route_w[L][s] = __builtin_bit_cast(float, (uint32_t)ww);
         }
+        break;
       }
+      if (++spins > kSpinLimit) {
+        fail_timeout();
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
     }
   }
   __syncthreads();
+  if (S.abort) {
+    finish();
+    return;
+  }
 
   // ---- per-wave prefetch state ----------------------------------------------
   // raw prefetched words: weights, f16 scale bits, zero-point byte + nibble
@@ -442,20 +453,21 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   u32x4 wa[kMaxRowsA];
   uint32_t sa[kMaxRowsA];
   uint32_t za[kMaxRowsA];
-  u32x4 wb[kMaxUnitsB];
-  uint32_t sb[kMaxUnitsB];
-  uint32_t zb[kMaxUnitsB];
-  // The prefetch keeps the aligned 32-bit words holding a lane's f16 scale
-  // (index gi) and u4 zero point (nibble gi); select them here.
+  u32x4 wb[3];
+  uint32_t sb[3];
+  uint32_t zb[3];
+  // norm weight (f32) and shared gate vector (f16) of this wave's 256 values
+  u32x4 nw;
+  u32x2 gv;
   auto nib = [](uint32_t word, int gi) { return (word >> ((gi & 7) * 4)) & 0xfu; };
   auto scl = [](uint32_t word, int gi) { return h2f((uint16_t)(word >> ((gi & 1) * 16))); };
 
   // Weight loads: scalar base (readfirstlane of the table pointer, so it is
   // provably wave-uniform) plus a 32-bit per-lane offset.  Each prefetch is
-  // straight-line code: a wave's surplus row slots are clamped onto a row the
-  // block loads anyway (a cache hit) and an out-of-range expert id onto
-  // expert 0 (its slot is weighted 0 and the error bit is set), so every
-  // load is in bounds and issued back to back.
+  // straight-line code: surplus row slots are clamped onto a row the block
+  // loads anyway (a cache hit) and an out-of-range expert id onto expert 0
+  // (its contribution is dropped and the error bit is set), so every load
+  // is in bounds and issued back to back.
   auto uptr = [](const void* p) {
     const uint64_t v = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
@@ -469,352 +481,380 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   auto ld_u32 = [](const AIMA_GLOBAL uint8_t* base_ptr, uint32_t off) {
     return *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base_ptr + off);
   };
-  // Per-lane offsets are recomputed at each prefetch from opaque copies of
-  // the lane and wave index: hoisting them out of the layer loop would keep
-  // ~30 more registers live across every phase.
+  // Per-lane offsets are recomputed at each prefetch from an opaque copy of
+  // the lane index: hoisting them out of the layer loop would keep many
+  // more registers live across every phase.
   auto opaque_v = [](int v) {
     asm volatile("" : "+v"(v));
     return v;
   };
-  auto opaque_s = [](int v) {
-    asm volatile("" : "+s"(v));
-    return v;
+  // the routed expert of this XCD in layer L (clamped to a valid id)
+  auto slot_expert = [&](int L) -> uint32_t {
+    const int e = x < k ? S.route_id[L][x] : 0;
+    return (uint32_t)max(0, __builtin_amdgcn_readfirstlane(e));
   };
-  const int rowsA = 2 * npairs;  // gate/up rows of this block
+  // gate/up rows: block row ri = 2 * (local pair) + (0 gate | 1 up); wave w
+  // takes ri = ((w + 4) & 7) + 8 i, so waves 4..7 carry the fifth row and the
+  // control duties of wave 0 fall on a wave with four
   auto prefetch_a = [&](int L) {
-    if (rowsA == 0) return;
-    const int lane = opaque_v(threadIdx.x & 63);
-    const int cw = opaque_s(wave - 1);
+    const int ln = opaque_v(threadIdx.x & 63);
     const aima_moe_layer& Ly = S.table[L];
+    const uint32_t e = slot_expert(L);
     const uint32_t wbytes = (uint32_t)(2 * kI) * (kH / 2);      // per expert
     const uint32_t sbytes = (uint32_t)(2 * kI) * gA * 2;
     const uint32_t zbytes = (uint32_t)(2 * kI) * gA / 2;
+    const AIMA_GLOBAL uint8_t* rw = uptr(Ly.gate_up.qweight) + (size_t)e * wbytes;
+    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.gate_up.scale) + (size_t)e * sbytes;
+    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.gate_up.zp) + (size_t)e * zbytes;
+    const AIMA_GLOBAL uint8_t* hw = uptr(Ly.shared_gate_up.qweight);
+    const AIMA_GLOBAL uint8_t* hs = uptr(Ly.shared_gate_up.scale);
+    const AIMA_GLOBAL uint8_t* hz = uptr(Ly.shared_gate_up.zp);
 #pragma unroll
     for (int i = 0; i < kMaxRowsA; ++i) {
-      const int ri = min(cw + kComputeWaves * i, rowsA - 1);  // row index within the block
-      const int pair = pair0 + (ri >> 1);
-      const int slot = pair / kI;
-      const int j = pair - slot * kI;
-      const int row = (ri & 1) ? kI + j : j;
-      const int gi = row * gA + ((lane * 32) >> glog2);
-      const bool routed = slot < k;
-      const uint32_t e =
-          (uint32_t)max(0, __builtin_amdgcn_readfirstlane(S.route_id[L][min(slot, k - 1)]));
-      const AIMA_GLOBAL uint8_t* w = routed ? uptr(Ly.gate_up.qweight) + (size_t)e * wbytes
-                                            : uptr(Ly.shared_gate_up.qweight);
-      const AIMA_GLOBAL uint8_t* sp = routed ? uptr(Ly.gate_up.scale) + (size_t)e * sbytes
-                                             : uptr(Ly.shared_gate_up.scale);
-      const AIMA_GLOBAL uint8_t* zp = routed ? uptr(Ly.gate_up.zp) + (size_t)e * zbytes
-                                             : uptr(Ly.shared_gate_up.zp);
-      wa[i] = ld_w(w, (uint32_t)row * (kH / 2) + lane * 16);
-      sa[i] = ld_u32(sp, (gi * 2) & ~3);
-      za[i] = ld_u32(zp, (gi >> 1) & ~3);
+      const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
+      const int p = j * kPairs + (ri >> 1);  // pair within the XCD
+      const bool routed = p < kI;
+      const int unit = routed ? p : x * kSlice + (p - kI);
+      const int row = (ri & 1) ? kI + unit : unit;
+      const int gi = row * gA + ((ln * 32) >> glog2);
+      wa[i] = ld_w(routed ? rw : hw, (uint32_t)row * (kH / 2) + ln * 16);
+      sa[i] = ld_u32(routed ? rs : hs, (gi * 2) & ~3);
+      za[i] = ld_u32(routed ? rz : hz, (gi >> 1) & ~3);
     }
   };
-  // B units: u = cw + 7 i -> slot = u / 2, pass = u % 2 (4 rows per pass)
+  // down rows: wave w owns block rows 8w .. 8w+7; units 0, 1 = routed rows
+  // 4u + (lane >> 4), chunk lane & 15; unit 2 = the shared slice, row
+  // (lane & 15) >> 1, chunk 2x + (lane & 1) of the full shared row
   auto prefetch_b = [&](int L) {
-    const int lane = opaque_v(threadIdx.x & 63);
-    const int cw = opaque_s(wave - 1);
+    const int ln = opaque_v(threadIdx.x & 63);
     const aima_moe_layer& Ly = S.table[L];
-    const int seg = lane >> 4, cl = lane & 15;
+    const uint32_t e = slot_expert(L);
     const uint32_t wbytes = (uint32_t)kH * (kI / 2);
     const uint32_t sbytes = (uint32_t)kH * gB * 2;
     const uint32_t zbytes = (uint32_t)kH * gB / 2;
+    const AIMA_GLOBAL uint8_t* rw = uptr(Ly.down.qweight) + (size_t)e * wbytes;
+    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.down.scale) + (size_t)e * sbytes;
+    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.down.zp) + (size_t)e * zbytes;
+    const int h0 = j * kRowsB + wave * kWaveRowsB;
 #pragma unroll
-    for (int i = 0; i < kMaxUnitsB; ++i) {
-      const int u = cw + kComputeWaves * i;
-      const int slot = min(u >> 1, slots - 1);
-      const int row = h0 + (u & 1) * 4 + seg;
+    for (int u = 0; u < 2; ++u) {
+      const int row = h0 + 4 * u + (ln >> 4);
+      const int cl = ln & 15;
       const int gi = row * gB + ((cl * 32) >> glog2);
-      const bool routed = slot < k;
-      const uint32_t e =
-          (uint32_t)max(0, __builtin_amdgcn_readfirstlane(S.route_id[L][min(slot, k - 1)]));
-      const AIMA_GLOBAL uint8_t* w = routed ? uptr(Ly.down.qweight) + (size_t)e * wbytes
-                                            : uptr(Ly.shared_down.qweight);
-      const AIMA_GLOBAL uint8_t* sp = routed ? uptr(Ly.down.scale) + (size_t)e * sbytes
-                                             : uptr(Ly.shared_down.scale);
-      const AIMA_GLOBAL uint8_t* zp = routed ? uptr(Ly.down.zp) + (size_t)e * zbytes
-                                             : uptr(Ly.shared_down.zp);
-      wb[i] = ld_w(w, (uint32_t)row * (kI / 2) + cl * 16);
-      sb[i] = ld_u32(sp, (gi * 2) & ~3);
-      zb[i] = ld_u32(zp, (gi >> 1) & ~3);
+      wb[u] = ld_w(rw, (uint32_t)row * (kI / 2) + cl * 16);
+      sb[u] = ld_u32(rs, (gi * 2) & ~3);
+      zb[u] = ld_u32(rz, (gi >> 1) & ~3);
+    }
+    {
+      const int row = h0 + ((ln & 15) >> 1);
+      const int ch = 2 * x + (ln & 1);
+      const int gi = row * gB + ((ch * 32) >> glog2);
+      wb[2] = ld_w(uptr(Ly.shared_down.qweight), (uint32_t)row * (kI / 2) + ch * 16);
+      sb[2] = ld_u32(uptr(Ly.shared_down.scale), (gi * 2) & ~3);
+      zb[2] = ld_u32(uptr(Ly.shared_down.zp), (gi >> 1) & ~3);
     }
   };
+  // this wave's 256 norm-weight floats and gate-vector halves: lane l holds
+  // values 256 w + 4 l .. +3
+  auto load_vec = [&](int L) {
+    const int ln = opaque_v(threadIdx.x & 63);
+    const aima_moe_layer& Ly = S.table[L];
+    const int v0 = wave * 256 + ln * 4;
+    nw = gload16(Ly.norm_weight + v0);
+    gv = *reinterpret_cast<const AIMA_GLOBAL u32x2*>(uptr(Ly.shared_gate_vec) + v0 * 2);
+  };
 
-  if (wave > 0) prefetch_a(0);
+  load_vec(0);
+  prefetch_a(0);
+  prefetch_b(0);
   AIMA_TRACE(40, 1, 0);  // prologue done
 
-  // r_{L} polling: eight coalesced 16-byte device-coherent loads per lane
-  // (the volatile bit keeps the compiler from merging repeated polls), one
-  // batch at a time without pause: measured faster than keeping two batches
-  // in flight or sleeping between polls, which add fabric traffic or delay.
-  constexpr int kAuxPoll = kAuxCoherent | (int)(1u << 31);
-  auto issue_r = [&](const AIMA_GLOBAL uint8_t* src, uint32_t (&rv)[32]) {
-    const int lane = opaque_v(threadIdx.x & 63);
-    const auto rr = __builtin_amdgcn_make_buffer_rsrc((void*)(uintptr_t)src, 0, kH * 4, 0x00020000);
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rr, (q * 64 + lane) * 16, 0, kAuxPoll);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) rv[4 * q + t] = v[t];
-    }
-  };
-  auto r_ready = [&](const uint32_t (&rv)[32], uint32_t ep) {
-    bool ok = true;
-#pragma unroll
-    for (int q = 0; q < 32; ++q) ok = ok && (rv[q] >> 16) == ep;
-    return __all(ok) != 0;
-  };
-  // act_L polling: 24 records per lane; each batch is staged into LDS as it
-  // is checked (a later complete batch overwrites it)
-  constexpr int kQ = kActRecords / 64;
-  const int nrec = (pairs + 2) / 3;  // valid records
-  auto issue_act = [&](const uint64_t* src, uint64_t (&v)[kQ]) {
-    const int lane = opaque_v(threadIdx.x & 63);
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) v[q] = ld_coherent64(src + lane + 64 * q);
-  };
-  auto stage_act = [&](const uint64_t (&v)[kQ], uint32_t ep) {
-    const int lane = opaque_v(threadIdx.x & 63);
-    bool ok = true;
-    uint8_t* d = reinterpret_cast<uint8_t*>(S.xb);
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) {
-      const int r = lane + 64 * q;
-      ok = ok && (r >= nrec || (uint32_t)(v[q] >> 48) == ep);
-      // record r = halves 3r..3r+2: an even r starts 4-byte aligned (word +
-      // half), an odd r ends 4-byte aligned (half + word)
-      const uint32_t lo = (uint32_t)v[q], hi = (uint32_t)(v[q] >> 32);
-      const bool even = (r & 1) == 0;
-      const uint32_t word = even ? lo : ((lo >> 16) | (hi << 16));
-      const uint16_t half = even ? (uint16_t)hi : (uint16_t)lo;
-      *reinterpret_cast<uint32_t*>(d + 6 * r + (even ? 0 : 2)) = word;
-      *reinterpret_cast<uint16_t*>(d + 6 * r + (even ? 4 : 0)) = half;
-    }
-    return __all(ok) != 0;
-  };
-
   for (int L = 0; L < a.n_layers; ++L) {
-    // an opaque lane index per layer keeps lane-derived addresses from being
-    // hoisted out of the loop (they would stay live in registers throughout)
-    const int lane = opaque_v(threadIdx.x & 63);
+    const int ln = opaque_v(threadIdx.x & 63);
     const uint32_t epA = base + 2u * (uint32_t)L;        // act_L
-    const uint32_t epB = base + 2u * (uint32_t)L + 1u;   // r_{L+1}
+    const uint32_t epP = base + 2u * (uint32_t)L + 1u;   // P_L
     const uint32_t epR = base + 2u * (uint32_t)L - 1u;   // r_L (L > 0)
+    const int par = L & 1;
 
     // ================= phase A_L =================
-    if (wave == 0) {
-      // r_L chunk `lane` as {f16, epoch} words
-      uint32_t rv[32];
-      if (L == 0) {
-        const AIMA_GLOBAL u32x4* p = (const AIMA_GLOBAL u32x4*)(a.r0 + lane * 32);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const u32x4 v = p[q];
-#pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            rv[8 * q + 2 * t] = v[t] & 0xffffu;
-            rv[8 * q + 2 * t + 1] = v[t] >> 16;
-          }
-        }
-      } else {
-        const AIMA_GLOBAL uint8_t* src = uptr(a.r_buf + ((L - 1) & 1) * kH);
-        uint32_t spins = 0;
-        while (true) {
-          issue_r(src, rv);
-          if (r_ready(rv, epR)) break;
-          if (++spins > kSpinLimit) {
-            fail_timeout();
-            break;
-          }
-        }
-      }
-      AIMA_TRACE(L, 0, 0);  // r_L polled
-      // RMSNorm: x = f16(r * rsqrt(mean(r^2) + eps) * w)
-      float ss = 0.f;
-#pragma unroll
-      for (int q = 0; q < 32; ++q) {
-        const float v = h2f((uint16_t)rv[q]);
-        ss += v * v;
-      }
-      ss = segment_sum<64>(ss);
-      const float scale = 1.0f / sqrtf(ss / (float)kH + a.eps);
-      uint32_t xw[16];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const u32x4 nv = S.nw_p[q][lane];
-#pragma unroll
-        for (int t = 0; t < 4; t += 2) {
-          const float n0 = as_f32(nv[t]);
-          const float n1 = as_f32(nv[t + 1]);
-          const uint16_t x0 = f2h(h2f((uint16_t)rv[4 * q + t]) * scale * n0);
-          const uint16_t x1 = f2h(h2f((uint16_t)rv[4 * q + t + 1]) * scale * n1);
-          xw[2 * q + t / 2] = (uint32_t)x0 | ((uint32_t)x1 << 16);
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        S.xw_p[q][lane] = u32x4{xw[4 * q], xw[4 * q + 1], xw[4 * q + 2], xw[4 * q + 3]};
-      }
-      XChunk c;
-      make_xchunk(xw, c);
-      put_chunk(S.xa_p, S.xa_bias, S.xa_xsum, lane, c);
-    }
-    __syncthreads();  // #1: A operands ready
-    AIMA_TRACE(L, 6, 64);
-    if (S.abort) {
-      finish();
-      return;
-    }
-    if (wave > 0) {
-      XChunk xc;
-      get_chunk(S.xa_p, S.xa_bias, S.xa_xsum, lane, xc);
-#pragma unroll
-      for (int i = 0; i < kMaxRowsA; ++i) {
-        const int ri = cw + kComputeWaves * i;
-        if ((ri >> 1) < npairs) {
-          const int pair = pair0 + (ri >> 1);
-          const int row = (ri & 1) ? kI + (pair % kI) : (pair % kI);
-          const int gi = row * gA + ((lane * 32) >> glog2);
-          const float d =
-              segment_sum<64>(u4_chunk_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
-          if (lane == 0) S.rowsum[ri] = d;
-        }
-      }
-      AIMA_TRACE(L, 7, 64);
+    // every wave reads its 256 values of r_L (one 16-byte load per lane)
+    uint32_t rv[4];
+    if (L == 0) {
+      const u32x2 v = *(const AIMA_GLOBAL u32x2*)(a.r0 + wave * 256 + ln * 4);
+      rv[0] = v[0] & 0xffffu;
+      rv[1] = v[0] >> 16;
+      rv[2] = v[1] & 0xffffu;
+      rv[3] = v[1] >> 16;
     } else {
-      // shared-expert gate sigma = sigmoid(gate_vec . x), every block for
-      // itself, while the compute waves run their dot products
-      float g = 0.f;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const u32x4 gg = S.gv_p[q][lane];
-        const u32x4 xx = S.xw_p[q][lane];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const f16x2 gh = as_h2(gg[t]);
-          const f16x2 xh = as_h2(xx[t]);
-          g += (float)gh.x * (float)xh.x;
-          g += (float)gh.y * (float)xh.y;
-        }
-      }
-      g = segment_sum<64>(g);
-      if (lane == 0) {
-        const double t = g;
-        S.sigma = (float)(t >= 0.0 ? 1.0 / (1.0 + exp(-t)) : exp(t) / (1.0 + exp(t)));
-      }
-    }
-    __syncthreads();  // #2: row sums ready
-    AIMA_TRACE(L, 1, 64);
-    u32x4 vec[2];
-    if (wave > 0) {
-      // SwiGLU for the block's pairs, published three per {3 x f16, epoch}
-      if (3 * ct < npairs) {
-        const int p0 = 3 * ct;
-        float rs[6];
-#pragma unroll
-        for (int j = 0; j < 6; ++j) rs[j] = S.rowsum[min(2 * p0 + j, kComputeWaves * kMaxRowsA - 1)];
-        uint64_t rec = (uint64_t)epA << 48;
-#pragma unroll
-        for (int j = 0; j < 3; ++j) {
-          const uint16_t h = p0 + j < npairs ? f2h(silu_mul(rs[2 * j], rs[2 * j + 1])) : (uint16_t)0;
-          rec |= (uint64_t)h << (16 * j);
-        }
-        st_coherent64(&a.act_buf[(L & 1) * kActRecords + pair0 / 3 + ct], rec);
-      }
-      AIMA_TRACE(L, 2, 64);
-      // Weight prefetches are issued where the compute waves would otherwise
-      // wait: a wave stalls at issue until the memory pipeline accepts its
-      // loads, which at the chip's streaming rate takes about a microsecond.
-      prefetch_b(L);
-      AIMA_TRACE(L, 8, 64);
-      if (L + 1 < a.n_layers) {
-        load_vec(L + 1, vec);
-        // the last compute wave fetches the next layer's route meanwhile
-        if (cw == kComputeWaves - 1 && !poll_route(L + 1)) fail_timeout();
-      }
-    } else {
-      const uint64_t* src = a.act_buf + (L & 1) * kActRecords;
-      uint64_t va[kQ];
+      const uint32_t* src = a.rx + ((size_t)x * 2 + par) * kH + wave * 256 + ln * 4;
       uint32_t spins = 0;
       while (true) {
-        issue_act(src, va);
-        if (stage_act(va, epA)) break;
+        const u32x4 v = poll1(src);
+        bool ok = true;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          rv[t] = v[t];
+          ok = ok && (v[t] >> 16) == epR;
+        }
+        if (__all(ok)) break;
         if (++spins > kSpinLimit) {
           fail_timeout();
           break;
         }
       }
-      AIMA_TRACE(L, 3, 0);
     }
-    __syncthreads();  // #3: act_L staged
-    AIMA_TRACE(L, 12, 64);
+    AIMA_TRACE(L, 0, 64);  // r_L read (wave 1)
+    float rf[4];
+    float ss = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      rf[t] = h2f((uint16_t)rv[t]);
+      ss += rf[t] * rf[t];
+    }
+    ss = segment_sum<64>(ss);
+    if (lane == 0) S.ss[wave] = ss;
+    *reinterpret_cast<u32x2*>(&S.rl[wave * 128 + ln * 2]) =
+        u32x2{(rv[0] & 0xffffu) | (rv[1] << 16), (rv[2] & 0xffffu) | (rv[3] << 16)};
+    __syncthreads();  // #1: r_L sums of squares
+    AIMA_TRACE(L, 1, 0);
     if (S.abort) {
       finish();
       return;
     }
-    if (wave > 0) {
-      // this wave's B operand chunks: lane t < 48 builds chunk (unit t/16, t%16)
-      if (lane < kChunksB) {
-        const int u = cw + kComputeWaves * (lane >> 4);
-        const int slot = u >> 1;
-        if (slot < slots) {
-          XChunk c;
-          lds_xchunk(S.xb, slot * (kI / 2) + (lane & 15) * 16, c);
-          put_chunk(S.xb_p[cw], S.xb_bias[cw], S.xb_xsum[cw], lane, c);
+    // RMSNorm: x = f16(r * rsqrt(mean(r^2) + eps) * w), this wave's values;
+    // lane l holds part l & 7 (values 4p .. 4p+3) of chunk 8w + (l >> 3)
+    {
+      float sst = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) sst += S.ss[w];
+      const float scale = 1.0f / sqrtf(sst / (float)kH + a.eps);
+      uint16_t xh[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xh[t] = f2h(rf[t] * scale * as_f32(nw[t]));
+      const uint32_t X0 = (uint32_t)xh[0] | ((uint32_t)xh[1] << 16);
+      const uint32_t X1 = (uint32_t)xh[2] | ((uint32_t)xh[3] << 16);
+      // partner lane (l ^ 1) holds the other half of the 8-value word group
+      const uint32_t Y0 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)X0, 0xB1, 0xF, 0xF, false);
+      const uint32_t Y1 = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)X1, 0xB1, 0xF, 0xF, false);
+      const bool hi = (ln & 1) != 0;
+      // low half (values 8d..8d+3): pairs (x0,x4), (x1,x5); high half: (x2,x6), (x3,x7)
+      const uint32_t lo_src = hi ? Y1 : X0;
+      const uint32_t hi_src = hi ? X1 : Y0;
+      const uint32_t p0 = __builtin_amdgcn_perm(hi_src, lo_src, 0x05040100u);
+      const uint32_t p1 = __builtin_amdgcn_perm(hi_src, lo_src, 0x07060302u);
+      const int c = wave * 8 + (ln >> 3);
+      const int d = (ln & 7) >> 1;
+      *reinterpret_cast<u32x2*>(reinterpret_cast<char*>(&S.xa_p[d][c]) + (hi ? 8 : 0)) =
+          u32x2{p0, p1};
+      float xe = h2f(xh[0]) + h2f(xh[2]);
+      float xo = h2f(xh[1]) + h2f(xh[3]);
+      xe = segment_sum<8>(xe);
+      xo = segment_sum<8>(xo);
+      if ((ln & 7) == 0) {
+        S.xa_bias[c] = 1024.f * xe + 64.f * xo;
+        S.xa_xsum[c] = xe + xo;
+      }
+      // shared-expert gate: partial dot of this wave's values
+      const f16x2 g0 = as_h2(gv[0]), g1 = as_h2(gv[1]);
+      float g = (float)g0.x * h2f(xh[0]);
+      g += (float)g0.y * h2f(xh[1]);
+      g += (float)g1.x * h2f(xh[2]);
+      g += (float)g1.y * h2f(xh[3]);
+      g = segment_sum<64>(g);
+      if (lane == 0) S.gp[wave] = g;
+    }
+    __syncthreads();  // #2: A operands ready
+    AIMA_TRACE(L, 2, 0);
+    {
+      XChunk xc;
+      get_chunk(S.xa_p, S.xa_bias, S.xa_xsum, ln, xc);
+#pragma unroll
+      for (int i = 0; i < kMaxRowsA; ++i) {
+        const int ri = ((wave + 4) & 7) + kWaves * i;
+        if (ri < kRowsA) {
+          const int p = j * kPairs + (ri >> 1);
+          const int unit = p < kI ? p : x * kSlice + (p - kI);
+          const int row = (ri & 1) ? kI + unit : unit;
+          const int gi = row * gA + ((ln * 32) >> glog2);
+          const float dd =
+              segment_sum<64>(u4_chunk_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
+          if (lane == 0) S.rowsum[ri] = dd;
         }
+      }
+    }
+    if (wave == 0) {
+      // shared-expert gate sigma = sigmoid(gate_vec . x), per block
+      float g = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) g += S.gp[w];
+      if (lane == 0) {
+        const double t = g;
+        S.sigma = (float)(t >= 0.0 ? 1.0 / (1.0 + exp(-t)) : exp(t) / (1.0 + exp(t)));
+      }
+    }
+    AIMA_TRACE(L, 3, 256);  // A dots done (wave 4)
+    __syncthreads();  // #3: row sums ready
+    AIMA_TRACE(L, 4, 0);
+    if (wave > 0 && L + 1 < a.n_layers) {
+      prefetch_a(L + 1);
+      load_vec(L + 1);
+    }
+    if (wave == 0) {
+      // SwiGLU for the block's 18 pairs, published three per record
+      if (lane < kPairs / 3) {
+        uint64_t rec = (uint64_t)epA << 48;
+#pragma unroll
+        for (int t = 0; t < 3; ++t) {
+          const int lp = 3 * lane + t;
+          rec |= (uint64_t)f2h(silu_mul(S.rowsum[2 * lp], S.rowsum[2 * lp + 1])) << (16 * t);
+        }
+        st_local64(&a.actx[((size_t)x * 2 + par) * kActStride + j * (kPairs / 3) + lane], rec);
+      }
+      AIMA_TRACE(L, 5, 0);  // act published
+      // act_L of this XCD: 192 records, lanes read records 2l, 2l+1 and
+      // 128 + 2(l & 31), +1
+      const uint64_t* src = a.actx + ((size_t)x * 2 + par) * kActStride;
+      const int r0 = 2 * ln, r1 = 128 + 2 * (ln & 31);
+      uint32_t spins = 0;
+      u32x4 v0, v1;
+      while (true) {
+        poll2(src + r0, src + r1, v0, v1);
+        const bool ok = (v0[1] >> 16) == epA && (v0[3] >> 16) == epA &&
+                        (v1[1] >> 16) == epA && (v1[3] >> 16) == epA;
+        if (__all(ok)) break;
+        if (++spins > kSpinLimit) {
+          fail_timeout();
+          break;
+        }
+      }
+      AIMA_TRACE(L, 6, 0);  // act_L read
+      // stage: record r holds act values 3r .. 3r+2 (f16 at byte 6r)
+      auto stage = [&](int r, uint32_t lo, uint32_t hi) {
+        uint8_t* d = reinterpret_cast<uint8_t*>(S.act);
+        const bool even = (r & 1) == 0;
+        const uint32_t word = even ? lo : ((lo >> 16) | (hi << 16));
+        const uint16_t half = even ? (uint16_t)hi : (uint16_t)lo;
+        *reinterpret_cast<uint32_t*>(d + 6 * r + (even ? 0 : 2)) = word;
+        *reinterpret_cast<uint16_t*>(d + 6 * r + (even ? 4 : 0)) = half;
+      };
+      stage(r0, v0[0], v0[1]);
+      stage(r0 + 1, v0[2], v0[3]);
+      if (ln < 32) {
+        stage(r1, v1[0], v1[1]);
+        stage(r1 + 1, v1[2], v1[3]);
       }
       wave_lds_sync();
-      AIMA_TRACE(L, 10, 64);
-      const int seg = lane >> 4, cl = lane & 15;
+      // B operands: lane c < 18 builds chunk c (16 routed, 2 shared)
+      if (ln < kChunksB) {
+        XChunk c;
+        lds_xchunk(S.act, ln * 16, c);
+        put_chunk(S.xb_p, S.xb_bias, S.xb_xsum, ln, c);
+      }
+    }
+    __syncthreads();  // #4: act_L operands staged
+    AIMA_TRACE(L, 7, 0);
+    if (S.abort) {
+      finish();
+      return;
+    }
+    // ================= phase B_L =================
+    {
+      const int h0 = j * kRowsB + wave * kWaveRowsB;
+      const int cl = ln & 15;
+      float dr[2];
 #pragma unroll
-      for (int i = 0; i < kMaxUnitsB; ++i) {
-        const int u = cw + kComputeWaves * i;
-        const int slot = u >> 1;
-        if (slot < slots) {
-          XChunk xc;
-          get_chunk(S.xb_p[cw], S.xb_bias[cw], S.xb_xsum[cw], i * 16 + cl, xc);
-          const int row = h0 + (u & 1) * 4 + seg;
-          const int gi = row * gB + ((cl * 32) >> glog2);
-          const float d =
-              segment_sum<16>(u4_chunk_dot(wb[i], xc, nib(zb[i], gi), scl(sb[i], gi), magic));
-          if (cl == 0) S.part[slot][(u & 1) * 4 + seg] = d;
+      for (int u = 0; u < 2; ++u) {
+        XChunk xc;
+        get_chunk(S.xb_p, S.xb_bias, S.xb_xsum, cl, xc);
+        const int row = h0 + 4 * u + (ln >> 4);
+        const int gi = row * gB + ((cl * 32) >> glog2);
+        dr[u] = segment_sum<16>(u4_chunk_dot(wb[u], xc, nib(zb[u], gi), scl(sb[u], gi), magic));
+      }
+      float ds;
+      {
+        XChunk xc;
+        get_chunk(S.xb_p, S.xb_bias, S.xb_xsum, kI / 32 + (ln & 1), xc);
+        const int row = h0 + ((ln & 15) >> 1);
+        const int ch = 2 * x + (ln & 1);
+        const int gi = row * gB + ((ch * 32) >> glog2);
+        ds = segment_sum<2>(u4_chunk_dot(wb[2], xc, nib(zb[2], gi), scl(sb[2], gi), magic));
+      }
+      // lane r < 8 gathers row r: routed sum from lane 16 (r & 3) of unit
+      // r >> 2, shared sum from lane 2r
+      const float g0 = __shfl(dr[0], (ln & 3) * 16, 64);
+      const float g1 = __shfl(dr[1], (ln & 3) * 16, 64);
+      const float gs = __shfl(ds, 2 * (ln & 7), 64);
+      const int eid = x < k ? S.route_id[L][x] : -1;
+      const float c = eid >= 0 ? S.route_w[L][x] : 0.f;
+      if (ln < kWaveRowsB) {
+        const float dsel = ln < 4 ? g0 : g1;
+        float pv = S.sigma * gs;
+        if (eid >= 0) pv = c * dsel + pv;
+        st_coherent64(&a.pbuf[((size_t)par * kH + h0 + ln) * kXcds + x], pack_f32(pv, epP));
+      }
+    }
+    AIMA_TRACE(L, 8, 0);  // P published (wave 0)
+    if (wave > 0 && L + 1 < a.n_layers) prefetch_b(L + 1);
+    if (wave == 0) {
+      // relay: rows 64j + lane of r_{L+1} = r_L + sum over XCDs of P
+      const uint64_t* src = a.pbuf + ((size_t)par * kH + j * kRowsB + ln) * kXcds;
+      u32x4 v[4];
+      uint32_t spins = 0;
+      bool have = true;
+      while (true) {
+        poll4(src, v);
+        bool ok = true;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ok = ok && v[q][1] == epP && v[q][3] == epP;
+        if (__all(ok)) break;
+        if (++spins > kSpinLimit) {
+          fail_timeout();
+          have = false;
+          break;
         }
       }
-      AIMA_TRACE(L, 11, 64);
-      if (L + 1 < a.n_layers) store_vec(vec);
-    }
-    __syncthreads();  // #4: partial sums ready, next layer's vectors staged
-    AIMA_TRACE(L, 4, 0);
-    if (wave > 0) {
-      if (L + 1 < a.n_layers) prefetch_a(L + 1);
-      AIMA_TRACE(L, 9, 64);
-    } else if (lane < kRowsB) {
-      // weighted sum in rank order, then the gated shared expert
-      float c[kMaxK], pv[kMaxSlots];
-#pragma unroll
-      for (int s = 0; s < kMaxK; ++s) {
-        c[s] = S.route_id[L][s] < 0 ? 0.f : S.route_w[L][s];
-        pv[s] = S.part[s][lane];
-      }
-      pv[kMaxK] = S.part[kMaxK][lane];
+      AIMA_TRACE(L, 9, 0);  // P read
+      // (as_f32 takes the word by value: __builtin_bit_cast applied directly
+      // to an element of a vector value reads element 0 with this compiler)
       float f = 0.f;
 #pragma unroll
-      for (int s = 0; s < kMaxK; ++s) {
-        if (s < k) f += c[s] * pv[s];
+      for (int q = 0; q < 4; ++q) {
+        f += as_f32(v[q][0]);
+        f += as_f32(v[q][2]);
       }
-      float sh = pv[0];
-#pragma unroll
-      for (int s = 1; s < kMaxSlots; ++s) sh = s == k ? pv[s] : sh;
-      f += S.sigma * sh;
-      const uint16_t o = f2h(S.rown[lane] + f);
-      S.rown[lane] = h2f(o);
+      const int h = j * kRowsB + ln;
+      const uint16_t rh = (uint16_t)(S.rl[h >> 1] >> ((h & 1) * 16));
+      const uint16_t o = f2h(h2f(rh) + f);
+      if (!have) {
+        // nothing is published after a timeout
+      } else if (L + 1 < a.n_layers) {
+        st_local32(&a.rx[((size_t)x * 2 + (par ^ 1)) * kH + h], pack_word(o, epP));
+      } else if (x == 0) {
+        a.out[h] = o;
+      }
+      AIMA_TRACE(L, 10, 0);  // r_{L+1} rows stored
+      // wave 0's weights for the next layer, in flight while r_{L+1} arrives
       if (L + 1 < a.n_layers) {
-        st_coherent32(&a.r_buf[(L & 1) * kH + r_pos(h0 + lane)], pack_word(o, epB));
-      } else {
-        a.out[h0 + lane] = o;
+        prefetch_a(L + 1);
+        load_vec(L + 1);
+        prefetch_b(L + 1);
       }
-      AIMA_TRACE(L, 5, 0);  // r_{L+1} rows stored
+    }
+  }
+  if (a.n_layers == 1 && b == 0 && wave == 0) {
+    // one layer: block 0 exits only after every block published P
+    const uint64_t* src = a.pbuf;
+    const uint32_t epP = base + 1u;
+    uint32_t spins = 0;
+    for (int h = lane; h < kH; h += 64) {
+      u32x4 v[4];
+      while (true) {
+        poll4(src + (size_t)h * kXcds, v);
+        bool ok = true;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) ok = ok && v[q][1] == epP && v[q][3] == epP;
+        if (ok || ++spins > kSpinLimit) break;
+      }
     }
   }
   finish();
@@ -843,8 +883,9 @@ struct aima_moe_decode_plan {
   int blocks = 0;
   char* mem = nullptr;  // device allocation holding everything below
   aima_moe_layer* table = nullptr;
-  uint32_t* r_buf = nullptr;
-  uint64_t* act_buf = nullptr;
+  uint32_t* rx = nullptr;
+  uint64_t* actx = nullptr;
+  uint64_t* pbuf = nullptr;
   uint32_t* route_ids = nullptr;
   uint64_t* route_w = nullptr;
   uint32_t* counter = nullptr;
@@ -905,11 +946,12 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   AIMA_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
   AIMA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_persistent_kernel,
                                                         kThreads, 0));
-  const int blocks = kH / kRowsB;  // 256: one block owns 8 output rows
-  if (!coop || (int64_t)cus * per_cu < blocks) {
+  const int blocks = kBlocks;  // one block per CU: 8 XCDs x 32 CUs
+  if (!coop || cus != kBlocks || per_cu < 1) {
     return fail(AIMA_E_UNSUPPORTED,
-                "moe_decode_plan_create: the device cannot keep 256 blocks of 512 threads "
-                "resident for a cooperative launch");
+                "moe_decode_plan_create: the persistent decode needs a device of 256 CUs "
+                "(8 XCDs x 32) that keeps one 512-thread block per CU resident for a "
+                "cooperative launch");
   }
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -919,8 +961,9 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   };
   const size_t o_err = take(kWsHeader);
   const size_t o_table = take(sizeof(aima_moe_layer) * n_layers);
-  const size_t o_r = take(sizeof(uint32_t) * 2 * kH);
-  const size_t o_act = take(sizeof(uint64_t) * 2 * kMaxSlots * kI / 3);
+  const size_t o_rx = take(sizeof(uint32_t) * kXcds * 2 * kH);
+  const size_t o_act = take(sizeof(uint64_t) * kXcds * 2 * kActStride);
+  const size_t o_p = take(sizeof(uint64_t) * 2 * kH * kXcds);
   const size_t o_rid = take(sizeof(uint32_t) * n_layers * k);
   const size_t o_rw = take(sizeof(uint64_t) * n_layers * k);
   const size_t o_ctr = take(256);
@@ -938,8 +981,9 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   }
   p->err = reinterpret_cast<uint32_t*>(p->mem + o_err);
   p->table = reinterpret_cast<aima_moe_layer*>(p->mem + o_table);
-  p->r_buf = reinterpret_cast<uint32_t*>(p->mem + o_r);
-  p->act_buf = reinterpret_cast<uint64_t*>(p->mem + o_act);
+  p->rx = reinterpret_cast<uint32_t*>(p->mem + o_rx);
+  p->actx = reinterpret_cast<uint64_t*>(p->mem + o_act);
+  p->pbuf = reinterpret_cast<uint64_t*>(p->mem + o_p);
   p->route_ids = reinterpret_cast<uint32_t*>(p->mem + o_rid);
   p->route_w = reinterpret_cast<uint64_t*>(p->mem + o_rw);
   p->counter = reinterpret_cast<uint32_t*>(p->mem + o_ctr);
@@ -983,8 +1027,9 @@ extern "C" int aima_moe_decode_plan_run(aima_moe_decode_plan* plan, float eps,
   a.eps = eps;
   a.r0 = residual_in;
   a.out = out;
-  a.r_buf = plan->r_buf;
-  a.act_buf = plan->act_buf;
+  a.rx = plan->rx;
+  a.actx = plan->actx;
+  a.pbuf = plan->pbuf;
   a.route_ids = plan->route_ids;
   a.route_w = plan->route_w;
   a.epoch_counter = plan->counter;
