@@ -94,7 +94,7 @@ struct PersistArgs {
   uint16_t* out;                  // f16 [H]
   uint32_t* rx;                   // [xcd][2][H]            {f16, epoch}, XCD-local
   uint64_t* actx;                 // [xcd][2][kActStride]   {3 x f16, epoch}, XCD-local
-  uint64_t* pbuf;                 // [2][H][xcd]            {f32, epoch}
+  uint64_t* pbuf;                 // [2][xcd][H]            {f32, epoch}
   uint32_t* route_ids;            // [L][k]                 {id, epoch}
   uint64_t* route_w;              // [L][k]                 {f32, epoch}
   uint32_t* epoch_counter;
@@ -136,14 +136,24 @@ __device__ __forceinline__ void poll2(const void* p, const void* q, u32x4& v, u3
       "s_waitcnt vmcnt(0)"
       : "=&v"(v), "=&v"(w) : "v"(p), "v"(q) : "memory");
 }
-__device__ __forceinline__ void poll4(const void* p, u32x4 (&v)[4]) {
+// eight 8-byte loads `stride` bytes apart
+__device__ __forceinline__ void poll8(const void* p, int stride, uint64_t (&v)[8]) {
+  const char* c = reinterpret_cast<const char*>(p);
   asm volatile(
-      "global_load_dwordx4 %0, %4, off sc1\n\t"
-      "global_load_dwordx4 %1, %4, off offset:16 sc1\n\t"
-      "global_load_dwordx4 %2, %4, off offset:32 sc1\n\t"
-      "global_load_dwordx4 %3, %4, off offset:48 sc1\n\t"
+      "global_load_dwordx2 %0, %8, off sc1\n\t"
+      "global_load_dwordx2 %1, %9, off sc1\n\t"
+      "global_load_dwordx2 %2, %10, off sc1\n\t"
+      "global_load_dwordx2 %3, %11, off sc1\n\t"
+      "global_load_dwordx2 %4, %12, off sc1\n\t"
+      "global_load_dwordx2 %5, %13, off sc1\n\t"
+      "global_load_dwordx2 %6, %14, off sc1\n\t"
+      "global_load_dwordx2 %7, %15, off sc1\n\t"
       "s_waitcnt vmcnt(0)"
-      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]) : "v"(p) : "memory");
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+        "=&v"(v[6]), "=&v"(v[7])
+      : "v"(c), "v"(c + stride), "v"(c + 2 * stride), "v"(c + 3 * stride), "v"(c + 4 * stride),
+        "v"(c + 5 * stride), "v"(c + 6 * stride), "v"(c + 7 * stride)
+      : "memory");
 }
 
 __device__ __forceinline__ uint32_t pack_word(uint16_t v, uint32_t epoch) {
@@ -790,22 +800,25 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
         const float dsel = ln < 4 ? g0 : g1;
         float pv = S.sigma * gs;
         if (eid >= 0) pv = c * dsel + pv;
-        st_coherent64(&a.pbuf[((size_t)par * kH + h0 + ln) * kXcds + x], pack_f32(pv, epP));
+        st_coherent64(&a.pbuf[((size_t)par * kXcds + x) * kH + h0 + ln], pack_f32(pv, epP));
       }
     }
     AIMA_TRACE(L, 8, 0);  // P published (wave 0)
     if (wave > 0 && L + 1 < a.n_layers) prefetch_b(L + 1);
     if (wave == 0) {
       // relay: rows 64j + lane of r_{L+1} = r_L + sum over XCDs of P
-      const uint64_t* src = a.pbuf + ((size_t)par * kH + j * kRowsB + ln) * kXcds;
-      u32x4 v[4];
+      // (each XCD's P rows are contiguous: stores from different XCDs never
+      // share a cache line, which measured 15 % faster per token than
+      // interleaving the 8 records of a row)
+      const uint64_t* src = a.pbuf + (size_t)par * kXcds * kH + j * kRowsB + ln;
+      uint64_t v[kXcds];
       uint32_t spins = 0;
       bool have = true;
       while (true) {
-        poll4(src, v);
+        poll8(src, kH * 8, v);
         bool ok = true;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ok = ok && v[q][1] == epP && v[q][3] == epP;
+        for (int q = 0; q < kXcds; ++q) ok = ok && (uint32_t)(v[q] >> 32) == epP;
         if (__all(ok)) break;
         if (++spins > kSpinLimit) {
           fail_timeout();
@@ -818,10 +831,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       // to an element of a vector value reads element 0 with this compiler)
       float f = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        f += as_f32(v[q][0]);
-        f += as_f32(v[q][2]);
-      }
+      for (int q = 0; q < kXcds; ++q) f += as_f32((uint32_t)v[q]);
       const int h = j * kRowsB + ln;
       const uint16_t rh = (uint16_t)(S.rl[h >> 1] >> ((h & 1) * 16));
       const uint16_t o = f2h(h2f(rh) + f);
@@ -843,16 +853,15 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   }
   if (a.n_layers == 1 && b == 0 && wave == 0) {
     // one layer: block 0 exits only after every block published P
-    const uint64_t* src = a.pbuf;
     const uint32_t epP = base + 1u;
     uint32_t spins = 0;
     for (int h = lane; h < kH; h += 64) {
-      u32x4 v[4];
+      uint64_t v[kXcds];
       while (true) {
-        poll4(src + (size_t)h * kXcds, v);
+        poll8(a.pbuf + h, kH * 8, v);
         bool ok = true;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) ok = ok && v[q][1] == epP && v[q][3] == epP;
+        for (int q = 0; q < kXcds; ++q) ok = ok && (uint32_t)(v[q] >> 32) == epP;
         if (ok || ++spins > kSpinLimit) break;
       }
     }
