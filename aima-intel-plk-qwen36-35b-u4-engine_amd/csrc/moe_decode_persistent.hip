@@ -459,16 +459,22 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
 
   // ---- per-wave prefetch state ----------------------------------------------
   // raw prefetched words: weights, f16 scale bits, zero-point byte + nibble
-  // shift; converted only when used so no wait sits between the loads
-  u32x4 wa[kMaxRowsA];
-  uint32_t sa[kMaxRowsA];
-  uint32_t za[kMaxRowsA];
-  u32x4 wb[3];
-  uint32_t sb[3];
-  uint32_t zb[3];
+  // shift; converted only when used so no wait sits between the loads.
+  // Double-buffered: the *_n registers receive the next layer's rows while
+  // the current ones are in use and are copied over at barrier #1.  The next
+  // layer's down rows and vectors are issued at barrier #2 and its gate/up
+  // rows one per dot product during A_L, so the stream overlaps the dot
+  // products (measured: issuing them next to the exchanges delays every poll
+  // behind them in the CU's memory pipeline).
+  u32x4 wa[kMaxRowsA], wa_n[kMaxRowsA];
+  uint32_t sa[kMaxRowsA], sa_n[kMaxRowsA];
+  uint32_t za[kMaxRowsA], za_n[kMaxRowsA];
+  u32x4 wb[3], wb_n[3];
+  uint32_t sb[3], sb_n[3];
+  uint32_t zb[3], zb_n[3];
   // norm weight (f32) and shared gate vector (f16) of this wave's 256 values
-  u32x4 nw;
-  u32x2 gv;
+  u32x4 nw, nw_n;
+  u32x2 gv, gv_n;
   auto nib = [](uint32_t word, int gi) { return (word >> ((gi & 7) * 4)) & 0xfu; };
   auto scl = [](uint32_t word, int gi) { return h2f((uint16_t)(word >> ((gi & 1) * 16))); };
 
@@ -505,7 +511,32 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   };
   // gate/up rows: block row ri = 2 * (local pair) + (0 gate | 1 up); wave w
   // takes ri = ((w + 4) & 7) + 8 i, so waves 4..7 carry the fifth row and the
-  // control duties of wave 0 fall on a wave with four
+  // control duties of wave 0 fall on a wave with four.  prefetch_a1 loads the
+  // wave's row slot i, prefetch_a all of them (a surplus slot is clamped onto
+  // the block's last row).
+  auto prefetch_a1 = [&](int L, int i) {
+    const int ln = opaque_v(threadIdx.x & 63);
+    const aima_moe_layer& Ly = S.table[L];
+    const uint32_t e = slot_expert(L);
+    const uint32_t wbytes = (uint32_t)(2 * kI) * (kH / 2);
+    const uint32_t sbytes = (uint32_t)(2 * kI) * gA * 2;
+    const uint32_t zbytes = (uint32_t)(2 * kI) * gA / 2;
+    const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
+    const int p = j * kPairs + (ri >> 1);
+    const bool routed = p < kI;
+    const AIMA_GLOBAL uint8_t* w = routed ? uptr(Ly.gate_up.qweight) + (size_t)e * wbytes
+                                          : uptr(Ly.shared_gate_up.qweight);
+    const AIMA_GLOBAL uint8_t* sp = routed ? uptr(Ly.gate_up.scale) + (size_t)e * sbytes
+                                           : uptr(Ly.shared_gate_up.scale);
+    const AIMA_GLOBAL uint8_t* zp = routed ? uptr(Ly.gate_up.zp) + (size_t)e * zbytes
+                                           : uptr(Ly.shared_gate_up.zp);
+    const int unit = routed ? p : x * kSlice + (p - kI);
+    const int row = (ri & 1) ? kI + unit : unit;
+    const int gi = row * gA + ((ln * 32) >> glog2);
+    wa_n[i] = ld_w(w, (uint32_t)row * (kH / 2) + ln * 16);
+    sa_n[i] = ld_u32(sp, (gi * 2) & ~3);
+    za_n[i] = ld_u32(zp, (gi >> 1) & ~3);
+  };
   auto prefetch_a = [&](int L) {
     const int ln = opaque_v(threadIdx.x & 63);
     const aima_moe_layer& Ly = S.table[L];
@@ -527,9 +558,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       const int unit = routed ? p : x * kSlice + (p - kI);
       const int row = (ri & 1) ? kI + unit : unit;
       const int gi = row * gA + ((ln * 32) >> glog2);
-      wa[i] = ld_w(routed ? rw : hw, (uint32_t)row * (kH / 2) + ln * 16);
-      sa[i] = ld_u32(routed ? rs : hs, (gi * 2) & ~3);
-      za[i] = ld_u32(routed ? rz : hz, (gi >> 1) & ~3);
+      wa_n[i] = ld_w(routed ? rw : hw, (uint32_t)row * (kH / 2) + ln * 16);
+      sa_n[i] = ld_u32(routed ? rs : hs, (gi * 2) & ~3);
+      za_n[i] = ld_u32(routed ? rz : hz, (gi >> 1) & ~3);
     }
   };
   // down rows: wave w owns block rows 8w .. 8w+7; units 0, 1 = routed rows
@@ -551,17 +582,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       const int row = h0 + 4 * u + (ln >> 4);
       const int cl = ln & 15;
       const int gi = row * gB + ((cl * 32) >> glog2);
-      wb[u] = ld_w(rw, (uint32_t)row * (kI / 2) + cl * 16);
-      sb[u] = ld_u32(rs, (gi * 2) & ~3);
-      zb[u] = ld_u32(rz, (gi >> 1) & ~3);
+      wb_n[u] = ld_w(rw, (uint32_t)row * (kI / 2) + cl * 16);
+      sb_n[u] = ld_u32(rs, (gi * 2) & ~3);
+      zb_n[u] = ld_u32(rz, (gi >> 1) & ~3);
     }
     {
       const int row = h0 + ((ln & 15) >> 1);
       const int ch = 2 * x + (ln & 1);
       const int gi = row * gB + ((ch * 32) >> glog2);
-      wb[2] = ld_w(uptr(Ly.shared_down.qweight), (uint32_t)row * (kI / 2) + ch * 16);
-      sb[2] = ld_u32(uptr(Ly.shared_down.scale), (gi * 2) & ~3);
-      zb[2] = ld_u32(uptr(Ly.shared_down.zp), (gi >> 1) & ~3);
+      wb_n[2] = ld_w(uptr(Ly.shared_down.qweight), (uint32_t)row * (kI / 2) + ch * 16);
+      sb_n[2] = ld_u32(uptr(Ly.shared_down.scale), (gi * 2) & ~3);
+      zb_n[2] = ld_u32(uptr(Ly.shared_down.zp), (gi >> 1) & ~3);
     }
   };
   // this wave's 256 norm-weight floats and gate-vector halves: lane l holds
@@ -570,8 +601,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     const int ln = opaque_v(threadIdx.x & 63);
     const aima_moe_layer& Ly = S.table[L];
     const int v0 = wave * 256 + ln * 4;
-    nw = gload16(Ly.norm_weight + v0);
-    gv = *reinterpret_cast<const AIMA_GLOBAL u32x2*>(uptr(Ly.shared_gate_vec) + v0 * 2);
+    nw_n = gload16(Ly.norm_weight + v0);
+    gv_n = *reinterpret_cast<const AIMA_GLOBAL u32x2*>(uptr(Ly.shared_gate_vec) + v0 * 2);
   };
 
   load_vec(0);
@@ -631,6 +662,20 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       finish();
       return;
     }
+#pragma unroll
+    for (int i = 0; i < kMaxRowsA; ++i) {
+      wa[i] = wa_n[i];
+      sa[i] = sa_n[i];
+      za[i] = za_n[i];
+    }
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      wb[u] = wb_n[u];
+      sb[u] = sb_n[u];
+      zb[u] = zb_n[u];
+    }
+    nw = nw_n;
+    gv = gv_n;
     // RMSNorm: x = f16(r * rsqrt(mean(r^2) + eps) * w), this wave's values;
     // lane l holds part l & 7 (values 4p .. 4p+3) of chunk 8w + (l >> 3)
     {
@@ -675,12 +720,19 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     }
     __syncthreads();  // #2: A operands ready
     AIMA_TRACE(L, 2, 0);
+    if (L + 1 < a.n_layers) {
+      load_vec(L + 1);
+      prefetch_b(L + 1);
+    }
     {
       XChunk xc;
       get_chunk(S.xa_p, S.xa_bias, S.xa_xsum, ln, xc);
 #pragma unroll
       for (int i = 0; i < kMaxRowsA; ++i) {
         const int ri = ((wave + 4) & 7) + kWaves * i;
+        // one row of the next layer per dot product (kept in place)
+        if (L + 1 < a.n_layers) prefetch_a1(L + 1, i);
+        __builtin_amdgcn_sched_barrier(0);
         if (ri < kRowsA) {
           const int p = j * kPairs + (ri >> 1);
           const int unit = p < kI ? p : x * kSlice + (p - kI);
@@ -705,10 +757,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     AIMA_TRACE(L, 3, 256);  // A dots done (wave 4)
     __syncthreads();  // #3: row sums ready
     AIMA_TRACE(L, 4, 0);
-    if (wave > 0 && L + 1 < a.n_layers) {
-      prefetch_a(L + 1);
-      load_vec(L + 1);
-    }
     if (wave == 0) {
       // SwiGLU for the block's 18 pairs, published three per record
       if (lane < kPairs / 3) {
@@ -804,7 +852,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       }
     }
     AIMA_TRACE(L, 8, 0);  // P published (wave 0)
-    if (wave > 0 && L + 1 < a.n_layers) prefetch_b(L + 1);
     if (wave == 0) {
       // relay: rows 64j + lane of r_{L+1} = r_L + sum over XCDs of P
       // (each XCD's P rows are contiguous: stores from different XCDs never
@@ -843,12 +890,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
         a.out[h] = o;
       }
       AIMA_TRACE(L, 10, 0);  // r_{L+1} rows stored
-      // wave 0's weights for the next layer, in flight while r_{L+1} arrives
-      if (L + 1 < a.n_layers) {
-        prefetch_a(L + 1);
-        load_vec(L + 1);
-        prefetch_b(L + 1);
-      }
     }
   }
   if (a.n_layers == 1 && b == 0 && wave == 0) {
