@@ -345,6 +345,9 @@ __device__ uint64_t* g_trace = nullptr;
 
 }  // namespace
 
+// G128: specialized for 128-wide quantization groups (gathered scale and
+// zero-point loads); the other instance serves every supported group size.
+template <bool G128>
 __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistArgs a) {
   __shared__ SharedState S;
   const int lane = threadIdx.x & 63;
@@ -475,6 +478,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // norm weight (f32) and shared gate vector (f16) of this wave's 256 values
   u32x4 nw, nw_n;
   u32x2 gv, gv_n;
+  // With 128-wide groups every scale and zero-point word a wave needs for a
+  // phase comes from one gathering load (lane q fetches word q of the list
+  // below) instead of two loads per row; the words are handed to the lanes
+  // that use them by ds_bpermute when the buffers rotate.  The per-row loads
+  // serve the other group sizes.
+  constexpr bool g128 = G128;
+  uint32_t gsa_n = 0, gsb_n = 0;
   auto nib = [](uint32_t word, int gi) { return (word >> ((gi & 7) * 4)) & 0xfu; };
   auto scl = [](uint32_t word, int gi) { return h2f((uint16_t)(word >> ((gi & 1) * 16))); };
 
@@ -509,6 +519,54 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     const int e = x < k ? S.route_id[L][x] : 0;
     return (uint32_t)max(0, __builtin_amdgcn_readfirstlane(e));
   };
+  // gate/up gather (groups of 128: 16 per row): lanes 0..39 = scale words
+  // 0..7 of row slots 0..4, lanes 40..49 = zero-point words 0..1 of row slots
+  // 0..4 (lanes above repeat lane 49)
+  auto gather_a = [&](int L) {
+    const int ln = opaque_v(threadIdx.x & 63);
+    const aima_moe_layer& Ly = S.table[L];
+    const uint32_t e = slot_expert(L);
+    const uint32_t sbytes = (uint32_t)(2 * kI) * 16 * 2;
+    const uint32_t zbytes = (uint32_t)(2 * kI) * 16 / 2;
+    const int q = min(ln, 49);
+    const bool is_s = q < 40;
+    const int i = is_s ? (q >> 3) : ((q - 40) >> 1);
+    const int w = is_s ? (q & 7) : ((q - 40) & 1);
+    const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
+    const int p = j * kPairs + (ri >> 1);
+    const bool routed = p < kI;
+    const int unit = routed ? p : x * kSlice + (p - kI);
+    const int row = (ri & 1) ? kI + unit : unit;
+    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.gate_up.scale) + (size_t)e * sbytes;
+    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.gate_up.zp) + (size_t)e * zbytes;
+    const AIMA_GLOBAL uint8_t* hs = uptr(Ly.shared_gate_up.scale);
+    const AIMA_GLOBAL uint8_t* hz = uptr(Ly.shared_gate_up.zp);
+    const AIMA_GLOBAL uint8_t* base = is_s ? (routed ? rs : hs) : (routed ? rz : hz);
+    const uint32_t off = is_s ? (uint32_t)row * 32 + 4 * w : (uint32_t)row * 8 + 4 * w;
+    gsa_n = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
+  };
+  // down gather (4 groups per row; the wave's 8 rows are consecutive):
+  // lanes 0..15 = routed scale words, 16..19 = routed zero-point words,
+  // 20..35 = shared scale words, 36..39 = shared zero-point words
+  auto gather_b = [&](int L) {
+    const int ln = opaque_v(threadIdx.x & 63);
+    const aima_moe_layer& Ly = S.table[L];
+    const uint32_t e = slot_expert(L);
+    const uint32_t sbytes = (uint32_t)kH * 4 * 2;
+    const uint32_t zbytes = (uint32_t)kH * 4 / 2;
+    const uint32_t h0 = (uint32_t)(j * kRowsB + wave * kWaveRowsB);
+    const int q = min(ln, 39);
+    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.down.scale) + (size_t)e * sbytes;
+    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.down.zp) + (size_t)e * zbytes;
+    const AIMA_GLOBAL uint8_t* hs = uptr(Ly.shared_down.scale);
+    const AIMA_GLOBAL uint8_t* hz = uptr(Ly.shared_down.zp);
+    const AIMA_GLOBAL uint8_t* base = q < 16 ? rs : q < 20 ? rz : q < 36 ? hs : hz;
+    const uint32_t off = q < 16   ? h0 * 8 + 4 * q
+                         : q < 20 ? h0 * 2 + 4 * (q - 16)
+                         : q < 36 ? h0 * 8 + 4 * (q - 20)
+                                  : h0 * 2 + 4 * (q - 36);
+    gsb_n = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
+  };
   // gate/up rows: block row ri = 2 * (local pair) + (0 gate | 1 up); wave w
   // takes ri = ((w + 4) & 7) + 8 i, so waves 4..7 carry the fifth row and the
   // control duties of wave 0 fall on a wave with four.  prefetch_a1 loads the
@@ -534,8 +592,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     const int row = (ri & 1) ? kI + unit : unit;
     const int gi = row * gA + ((ln * 32) >> glog2);
     wa_n[i] = ld_w(w, (uint32_t)row * (kH / 2) + ln * 16);
-    sa_n[i] = ld_u32(sp, (gi * 2) & ~3);
-    za_n[i] = ld_u32(zp, (gi >> 1) & ~3);
+    if (g128) {
+      if (i == 0) gather_a(L);
+    } else {
+      sa_n[i] = ld_u32(sp, (gi * 2) & ~3);
+      za_n[i] = ld_u32(zp, (gi >> 1) & ~3);
+    }
   };
   auto prefetch_a = [&](int L) {
     const int ln = opaque_v(threadIdx.x & 63);
@@ -559,9 +621,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       const int row = (ri & 1) ? kI + unit : unit;
       const int gi = row * gA + ((ln * 32) >> glog2);
       wa_n[i] = ld_w(routed ? rw : hw, (uint32_t)row * (kH / 2) + ln * 16);
-      sa_n[i] = ld_u32(routed ? rs : hs, (gi * 2) & ~3);
-      za_n[i] = ld_u32(routed ? rz : hz, (gi >> 1) & ~3);
+      if (!g128) {
+        sa_n[i] = ld_u32(routed ? rs : hs, (gi * 2) & ~3);
+        za_n[i] = ld_u32(routed ? rz : hz, (gi >> 1) & ~3);
+      }
     }
+    if (g128) gather_a(L);
   };
   // down rows: wave w owns block rows 8w .. 8w+7; units 0, 1 = routed rows
   // 4u + (lane >> 4), chunk lane & 15; unit 2 = the shared slice, row
@@ -583,17 +648,22 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       const int cl = ln & 15;
       const int gi = row * gB + ((cl * 32) >> glog2);
       wb_n[u] = ld_w(rw, (uint32_t)row * (kI / 2) + cl * 16);
-      sb_n[u] = ld_u32(rs, (gi * 2) & ~3);
-      zb_n[u] = ld_u32(rz, (gi >> 1) & ~3);
+      if (!g128) {
+        sb_n[u] = ld_u32(rs, (gi * 2) & ~3);
+        zb_n[u] = ld_u32(rz, (gi >> 1) & ~3);
+      }
     }
     {
       const int row = h0 + ((ln & 15) >> 1);
       const int ch = 2 * x + (ln & 1);
       const int gi = row * gB + ((ch * 32) >> glog2);
       wb_n[2] = ld_w(uptr(Ly.shared_down.qweight), (uint32_t)row * (kI / 2) + ch * 16);
-      sb_n[2] = ld_u32(uptr(Ly.shared_down.scale), (gi * 2) & ~3);
-      zb_n[2] = ld_u32(uptr(Ly.shared_down.zp), (gi >> 1) & ~3);
+      if (!g128) {
+        sb_n[2] = ld_u32(uptr(Ly.shared_down.scale), (gi * 2) & ~3);
+        zb_n[2] = ld_u32(uptr(Ly.shared_down.zp), (gi >> 1) & ~3);
+      }
     }
+    if (g128) gather_b(L);
   };
   // this wave's 256 norm-weight floats and gate-vector halves: lane l holds
   // values 256 w + 4 l .. +3
@@ -663,16 +733,40 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       return;
     }
 #pragma unroll
-    for (int i = 0; i < kMaxRowsA; ++i) {
-      wa[i] = wa_n[i];
-      sa[i] = sa_n[i];
-      za[i] = za_n[i];
-    }
+    for (int i = 0; i < kMaxRowsA; ++i) wa[i] = wa_n[i];
 #pragma unroll
-    for (int u = 0; u < 3; ++u) {
-      wb[u] = wb_n[u];
-      sb[u] = sb_n[u];
-      zb[u] = zb_n[u];
+    for (int u = 0; u < 3; ++u) wb[u] = wb_n[u];
+    if (g128) {
+      // lane l: gate/up group l / 4 of row slot i; down routed row
+      // 4u + l / 16, group (l & 15) / 4; shared row (l & 15) / 2, group x / 2
+      auto pick = [](uint32_t v, int src) {
+        return (uint32_t)__builtin_amdgcn_ds_bpermute(src * 4, (int)v);
+      };
+#pragma unroll
+      for (int i = 0; i < kMaxRowsA; ++i) {
+        sa[i] = pick(gsa_n, 8 * i + (ln >> 3));
+        za[i] = pick(gsa_n, 40 + 2 * i + (ln >> 5));
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = 4 * u + (ln >> 4);
+        sb[u] = pick(gsb_n, 2 * r + ((ln & 15) >> 3));
+        zb[u] = pick(gsb_n, 16 + (r >> 1));
+      }
+      const int r8 = (ln & 15) >> 1;
+      sb[2] = pick(gsb_n, 20 + 2 * r8 + (x >> 2));
+      zb[2] = pick(gsb_n, 36 + (r8 >> 1));
+    } else {
+#pragma unroll
+      for (int i = 0; i < kMaxRowsA; ++i) {
+        sa[i] = sa_n[i];
+        za[i] = za_n[i];
+      }
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        sb[u] = sb_n[u];
+        zb[u] = zb_n[u];
+      }
     }
     nw = nw_n;
     gv = gv_n;
@@ -994,8 +1088,12 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   int cus = 0, coop = 0, per_cu = 0;
   AIMA_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   AIMA_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
-  AIMA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_persistent_kernel,
+  int per_cu128 = 0;
+  AIMA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_persistent_kernel<false>,
                                                         kThreads, 0));
+  AIMA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+      &per_cu128, decode_persistent_kernel<true>, kThreads, 0));
+  per_cu = std::min(per_cu, per_cu128);
   const int blocks = kBlocks;  // one block per CU: 8 XCDs x 32 CUs
   if (!coop || cus != kBlocks || per_cu < 1) {
     return fail(AIMA_E_UNSUPPORTED,
@@ -1085,7 +1183,10 @@ extern "C" int aima_moe_decode_plan_run(aima_moe_decode_plan* plan, float eps,
   a.epoch_counter = plan->counter;
   a.err = plan->err;
   void* args[] = {&a};
-  AIMA_HIP(hipLaunchCooperativeKernel(reinterpret_cast<const void*>(decode_persistent_kernel),
+  const void* kern = plan->group_log2 == 7
+                         ? reinterpret_cast<const void*>(decode_persistent_kernel<true>)
+                         : reinterpret_cast<const void*>(decode_persistent_kernel<false>);
+  AIMA_HIP(hipLaunchCooperativeKernel(kern,
                                       dim3(plan->blocks), dim3(kThreads), args, 0, st));
   return AIMA_OK;
 }

@@ -213,6 +213,26 @@ def test_decode_plan_small_stack(pkg, dev):
         assert_parity(f16_to_f32(a), oracle.f16_values(ref[0]), what=f"plan small rep={rep}")
 
 
+@pytest.mark.parametrize("group", [64, 256])
+def test_decode_plan_other_groups(pkg, dev, group):
+    """Group sizes other than 128 run the general kernel instance (per-row
+    scale and zero-point loads): 2 layers of the real width vs the oracle."""
+    layers = [pkg.synth.moe_layer(hidden=2048, inter=512, experts=16, group=group,
+                                  seed=980 + l, device=dev) for l in range(2)]
+    lnp = [moe_to_oracle(l) for l in layers]
+    norms = [l.norm_weight.cpu().numpy() for l in layers]
+    plan = pkg.DecodePlan(layers, k=8)
+    x = pkg.synth.activations(1, 2048, 90, dev)
+    logits = torch.stack([pkg.synth.router_logits(1, 16, 91 + l, dev)[0] for l in range(2)])
+    ids, w = pkg.select_router_topk(logits, 8)
+    out = plan.run(x[0], router_logits=logits)
+    torch.cuda.synchronize()
+    assert plan.error_bits() == 0
+    ref = oracle_stack(lnp, norms, f16_bits(x), ids.cpu().numpy()[:, None],
+                       w.cpu().numpy()[:, None])
+    assert_parity(f16_to_f32(out), oracle.f16_values(ref[0]), what=f"plan group {group}")
+
+
 def test_decode_plan_flags_bad_ids(pkg, dev):
     layers = make_stack(pkg, dev, 2, 2048, 512, 16, seed=950)
     plan = pkg.DecodePlan(layers, k=8)
