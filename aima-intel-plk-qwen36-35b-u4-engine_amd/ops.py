@@ -327,7 +327,7 @@ class DecodePlan:
 
     Mirrors the reference's resident native loop: ``DecodePlan(layers, k)``
     uploads the layer table once; ``run`` executes RMSNorm -> MoE FFN ->
-    residual for every layer in a single cooperative kernel (graph-capturable,
+    residual for every layer in a single persistent kernel (graph-capturable,
     no allocation).  Routing comes from ``router_logits`` [L, E] (the
     select_router_topk rule) or from ``ids``/``weights`` [L, k].
     Raises AimaError(AIMA_E_UNSUPPORTED) for shapes outside the specialization

@@ -220,16 +220,21 @@ int aima_moe_stack_decode(const aima_moe_layer* layers, int32_t n_layers,
                           size_t workspace_bytes, void* stream);
 
 /* Resident decode plan: the whole n_layers-layer decode step in ONE
- * cooperative launch (hidden 2048, inter 512, k <= 8; see
+ * persistent launch (hidden 2048, inter 512, k <= 8; see
  * moe_decode_persistent.hip).  create() validates the shapes, checks that
- * the device keeps 256 blocks of 512 threads resident, allocates the plan's
+ * the device has 256 CUs (8 XCDs x 32) and keeps one 512-thread block
+ * resident on each, allocates the plan's
  * device buffers and uploads the layer table (synchronous, setup time only;
  * AIMA_E_UNSUPPORTED when the shape or device does not fit, in which case
  * aima_moe_stack_decode is the general path).  run() is asynchronous,
  * allocates nothing and can be captured in a HIP graph: routing comes from
  * router_logits [n_layers][experts] (the select_router_topk rule) or, when
  * that is NULL, from ids/weights [n_layers][k]; out = r_{n_layers} as in
- * aima_moe_stack_decode.  Calls on one plan must not overlap.  Mirrors the
+ * aima_moe_stack_decode.  Calls on one plan must not overlap, and no other
+ * plan's run may execute concurrently on the same device (another stream):
+ * all 256 blocks must be resident at once, and two persistent launches
+ * sharing the CUs can each wait for blocks the other holds, which the
+ * kernel's spin limits report as AIMA_DEVERR_TIMEOUT.  Mirrors the
  * reference's resident native loop (engine/include/intel_qwen36/
  * native_carrier_loop.hpp:38-100) for the MoE FFN stack. */
 typedef struct aima_moe_decode_plan aima_moe_decode_plan;
