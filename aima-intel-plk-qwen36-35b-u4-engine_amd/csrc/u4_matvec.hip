@@ -6,7 +6,8 @@
 // issues one 128-bit global load per row, unpacks in registers and reduces
 // with two v_dot2_f32_f16 chains (see XChunk in common.h), then the row's
 // segment is reduced across lanes.  Row groups are loaded before any compute
-// so each wave keeps RG x 1 KB in flight.
+// so each wave keeps RG x 1 KB in flight; the block's scales and zero points
+// (contiguous, its rows being consecutive) are staged through LDS.
 #include "common.h"
 
 #include <math.h>
@@ -76,44 +77,55 @@ __global__ __launch_bounds__(256) void u4_matvec_kernel(
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zp,
     int64_t n, int group_log2, void* __restrict__ y, int out_f32) {
   using G = RowGeom<KCH>;
+  constexpr int BR = 4 * RG * G::RPI;       // rows of the block (consecutive)
+  constexpr int kMaxGroups = G::K / 32;     // groups per row at group 32
+  // The block's scales and zero points are contiguous: staged through LDS
+  // with one element per thread (a scale and a zero-point load per lane and
+  // row would cost two memory instructions per 16-byte weight load).
+  __shared__ uint16_t s_lds[BR * kMaxGroups];
+  __shared__ uint8_t z_lds[BR * kMaxGroups / 2];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int seg = lane / G::SEG;
   const int cl = lane % G::SEG;
-  const int64_t groups = (int64_t)G::K >> group_log2;
+  const int groups = G::K >> group_log2;
   const uint32_t magic = u4_magic();
 
-  XChunk xc[G::NC];
-  load_x_chunks<KCH>(x, cl, xc);
-
-  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * (RG * G::RPI);
+  const int64_t brow0 = (int64_t)blockIdx.x * BR;
+  const int64_t row0 = brow0 + (int64_t)wave * (RG * G::RPI);
   u32x4 w[RG][G::NC];
-  float s[RG][G::NC];
-  uint32_t z[RG][G::NC];
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
     const int64_t row = row0 + r * G::RPI + seg;
 #pragma unroll
     for (int i = 0; i < G::NC; ++i) {
       const int c = cl + i * G::SEG;
-      if (row < n) {
-        w[r][i] = load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16);
-        const int64_t gi = row * groups + (((int64_t)c * 32) >> group_log2);
-        s[r][i] = h2f(scale[gi]);
-        z[r][i] = u4_code(zp, gi);
-      } else {
-        w[r][i] = u32x4{0u, 0u, 0u, 0u};
-        s[r][i] = 0.f;
-        z[r][i] = 0u;
-      }
+      w[r][i] = row < n ? load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16)
+                        : u32x4{0u, 0u, 0u, 0u};
     }
   }
+  {
+    const int64_t rows_here = n - brow0 < BR ? n - brow0 : BR;
+    const int nsc = (int)rows_here * groups;  // scales (and zero-point nibbles) of the block
+    for (int t = threadIdx.x; t < nsc; t += 256) s_lds[t] = scale[brow0 * groups + t];
+    for (int t = threadIdx.x; t < (nsc + 1) / 2; t += 256) z_lds[t] = zp[(brow0 * groups >> 1) + t];
+  }
+  XChunk xc[G::NC];
+  load_x_chunks<KCH>(x, cl, xc);
+  __syncthreads();
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
-    const int64_t row = row0 + r * G::RPI + seg;
+    const int rl = wave * (RG * G::RPI) + r * G::RPI + seg;  // row within the block
+    const int64_t row = brow0 + rl;
     float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < G::NC; ++i) acc += u4_chunk_dot(w[r][i], xc[i], z[r][i], s[r][i], magic);
+    for (int i = 0; i < G::NC; ++i) {
+      const int c = cl + i * G::SEG;
+      const int gi = rl * groups + ((c * 32) >> group_log2);
+      const float sv = row < n ? h2f(s_lds[gi]) : 0.f;
+      const uint32_t zv = row < n ? (uint32_t)(z_lds[gi >> 1] >> ((gi & 1) * 4)) & 0xfu : 0u;
+      acc += u4_chunk_dot(w[r][i], xc[i], zv, sv, magic);
+    }
     acc = segment_sum<G::SEG>(acc);
     if (cl == 0 && row < n) {
       if (out_f32) {
@@ -129,11 +141,18 @@ template <int KCH>
 static void launch_matvec(const uint16_t* x, const uint8_t* qw, const uint16_t* scale,
                           const uint8_t* zp, int64_t n, int glog2, void* y, int out_f32,
                           hipStream_t st) {
-  constexpr int RG = 4;
-  const int64_t rows_per_block = 4 * RG * RowGeom<KCH>::RPI;
-  const int64_t blocks = (n + rows_per_block - 1) / rows_per_block;
-  hipLaunchKernelGGL((u4_matvec_kernel<KCH, RG>), dim3((unsigned)blocks), dim3(256), 0, st,
-                     x, qw, scale, zp, n, glog2, y, out_f32);
+  // 8 row passes per wave (8 KB in flight per wave at K = 2048) once that
+  // still leaves two blocks per CU; 4 below (measured at N = 248320: 13 %
+  // faster than 4 passes, slower at 12 or 16)
+  const int64_t rows8 = 4 * 8 * RowGeom<KCH>::RPI;
+  if ((n + rows8 - 1) / rows8 >= 512) {
+    hipLaunchKernelGGL((u4_matvec_kernel<KCH, 8>), dim3((unsigned)((n + rows8 - 1) / rows8)),
+                       dim3(256), 0, st, x, qw, scale, zp, n, glog2, y, out_f32);
+  } else {
+    const int64_t rows4 = 4 * 4 * RowGeom<KCH>::RPI;
+    hipLaunchKernelGGL((u4_matvec_kernel<KCH, 4>), dim3((unsigned)((n + rows4 - 1) / rows4)),
+                       dim3(256), 0, st, x, qw, scale, zp, n, glog2, y, out_f32);
+  }
 }
 
 // ---------------------------------------------------------------------------

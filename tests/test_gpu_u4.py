@@ -64,6 +64,16 @@ def test_matvec_groups(pkg, dev, group):
     assert c["max_rel"] < 1e-4, c
 
 
+@pytest.mark.parametrize("k,rows,group", [(2048, 20001, 64), (512, 70001, 32),
+                                           (4096, 17001, 256), (128, 300001, 128)])
+def test_matvec_many_rows(pkg, dev, k, rows, group):
+    """Row counts that take the 8-pass kernel instance, with a partial last
+    block (scales and zero points staged per block)."""
+    got, ref = _matvec_case(pkg, dev, rows, k, group, seed=rows, out_dtype=torch.float32)
+    c = assert_parity(got, ref, what=f"k={k} rows={rows} group={group}")
+    assert c["max_rel"] < 1e-4, c
+
+
 def test_config3_lm_head(pkg, dev):
     """K=2048, N=248320 (vocab rows), f32 logits."""
     got, ref = _matvec_case(pkg, dev, 248320, 2048, 128, seed=3, out_dtype=torch.float32)
