@@ -236,7 +236,9 @@ __device__ __forceinline__ float block_sum_256(float v, float* red) {
 // Row helpers for 256-thread blocks over an f16 row of H elements (H a
 // multiple of 8, row 16-byte aligned): thread i handles the 8-element chunks
 // i, i + 256, ... with 16-byte accesses.  Every caller of a helper sums in
-// the same order, so fused and standalone uses agree bit for bit.
+// the same order with explicit fused multiply-adds (fmaf: the compiler's own
+// contraction depends on the surrounding code), so fused and standalone uses
+// agree bit for bit.
 __device__ __forceinline__ float row_dot_f16(const uint16_t* __restrict__ a,
                                              const uint16_t* __restrict__ b, int64_t H,
                                              float* red) {
@@ -246,8 +248,8 @@ __device__ __forceinline__ float row_dot_f16(const uint16_t* __restrict__ a,
     const u32x4 vb = *reinterpret_cast<const u32x4*>(b + i);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      s += h2f((uint16_t)(va[j] & 0xffffu)) * h2f((uint16_t)(vb[j] & 0xffffu));
-      s += h2f((uint16_t)(va[j] >> 16)) * h2f((uint16_t)(vb[j] >> 16));
+      s = fmaf(h2f((uint16_t)(va[j] & 0xffffu)), h2f((uint16_t)(vb[j] & 0xffffu)), s);
+      s = fmaf(h2f((uint16_t)(va[j] >> 16)), h2f((uint16_t)(vb[j] >> 16)), s);
     }
   }
   return block_sum_256(s, red);
@@ -263,8 +265,8 @@ __device__ __forceinline__ void rmsnorm_row(const uint16_t* __restrict__ x,
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float lo = h2f((uint16_t)(v[j] & 0xffffu)), hi = h2f((uint16_t)(v[j] >> 16));
-      ss += lo * lo;
-      ss += hi * hi;
+      ss = fmaf(lo, lo, ss);
+      ss = fmaf(hi, hi, ss);
     }
   }
   ss = block_sum_256(ss, red);

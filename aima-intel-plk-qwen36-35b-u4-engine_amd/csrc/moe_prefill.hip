@@ -33,7 +33,7 @@
 namespace aima {
 
 constexpr int kBM = 256;            // rows per M tile (8 MFMA blocks of 32)
-constexpr int kSchedBlock = 256;    // assignments per schedule block
+constexpr int kSchedBlock = 1024;   // assignments per schedule block
 constexpr int kMaxExperts = 1024;
 constexpr int kTileClasses = 8;     // tile heights 32, 64, ..., 256 rows
 
@@ -768,8 +768,8 @@ __global__ __launch_bounds__(256) void combine_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t wj = c[j];
-      o[2 * j] = s[2 * j] + h2f((uint16_t)(wj & 0xffffu)) * sigma;
-      o[2 * j + 1] = s[2 * j + 1] + h2f((uint16_t)(wj >> 16)) * sigma;
+      o[2 * j] = fmaf(h2f((uint16_t)(wj & 0xffffu)), sigma, s[2 * j]);
+      o[2 * j + 1] = fmaf(h2f((uint16_t)(wj >> 16)), sigma, s[2 * j + 1]);
     }
     if (residual) {
       const u32x4 rv = *reinterpret_cast<const u32x4*>(residual + t * H + h);
@@ -793,6 +793,103 @@ __global__ __launch_bounds__(256) void combine_kernel(
     if (threadIdx.x == 0) next.sigma[t] = sn;
   }
 }
+
+// combine_kernel for H = 2048 and k <= 8 (one 16-byte chunk per thread):
+// every load is issued before any use, the rank order comes from the
+// inverse map read directly (uniform), and the fused next-layer RMSNorm and
+// gate work from the registers just written.  Arithmetic and summation
+// order are those of combine_kernel + rmsnorm_row + row_dot_f16, so the two
+// kernels agree bit for bit.
+__global__ __launch_bounds__(256) void combine2048_kernel(
+    const uint16_t* __restrict__ contrib, const int32_t* __restrict__ inverse_map, int k,
+    int64_t A, const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate_vec,
+    const float* __restrict__ sigma_in, const uint16_t* __restrict__ residual,
+    uint16_t* __restrict__ out, CombineNext next) {
+  constexpr int64_t H = 2048;
+  constexpr int kMaxK = 8;
+  __shared__ float red[4];
+  const int64_t t = blockIdx.x;
+  const int h = threadIdx.x * 8;
+  u32x4 cr[kMaxK];
+#pragma unroll
+  for (int r = 0; r < kMaxK; ++r) {
+    const int64_t row = inverse_map[t * k + (r < k ? r : k - 1)];
+    cr[r] = *reinterpret_cast<const u32x4*>(contrib + row * H + h);
+  }
+  const u32x4 cs = *reinterpret_cast<const u32x4*>(contrib + (A + t) * H + h);
+  const u32x4 rv = residual ? *reinterpret_cast<const u32x4*>(residual + t * H + h)
+                            : u32x4{0u, 0u, 0u, 0u};
+  u32x4 nw0{}, nw1{}, ng{};
+  if (next.norm) {
+    nw0 = *reinterpret_cast<const u32x4*>(next.norm + h);
+    nw1 = *reinterpret_cast<const u32x4*>(next.norm + h + 4);
+    ng = *reinterpret_cast<const u32x4*>(next.gate_vec + h);
+  }
+  const float sigma = sigma_in ? sigma_in[t] : shared_gate_sigma(gate_vec, x + t * H, H, red);
+  float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < kMaxK; ++r) {
+    if (r < k) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t wj = cr[r][j];
+        s[2 * j] += h2f((uint16_t)(wj & 0xffffu));
+        s[2 * j + 1] += h2f((uint16_t)(wj >> 16));
+      }
+    }
+  }
+  float o[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t wj = cs[j];
+    o[2 * j] = fmaf(h2f((uint16_t)(wj & 0xffffu)), sigma, s[2 * j]);
+    o[2 * j + 1] = fmaf(h2f((uint16_t)(wj >> 16)), sigma, s[2 * j + 1]);
+  }
+  if (residual) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t wj = rv[j];
+      o[2 * j] = h2f((uint16_t)(wj & 0xffffu)) + o[2 * j];
+      o[2 * j + 1] = h2f((uint16_t)(wj >> 16)) + o[2 * j + 1];
+    }
+  }
+  u32x4 ov;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) ov[j] = pack_h2(o[2 * j], o[2 * j + 1]);
+  *reinterpret_cast<u32x4*>(out + t * H + h) = ov;
+  if (next.norm) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = h2f((uint16_t)(ov[j] & 0xffffu)), hi = h2f((uint16_t)(ov[j] >> 16));
+      ss = fmaf(lo, lo, ss);
+      ss = fmaf(hi, hi, ss);
+    }
+    ss = block_sum_256(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)H + next.eps);
+    const float wv[8] = {as_f32(nw0[0]), as_f32(nw0[1]), as_f32(nw0[2]), as_f32(nw0[3]),
+                         as_f32(nw1[0]), as_f32(nw1[1]), as_f32(nw1[2]), as_f32(nw1[3])};
+    u32x4 hv;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float lo = h2f((uint16_t)(ov[j] & 0xffffu)) * scale * wv[2 * j];
+      const float hi = h2f((uint16_t)(ov[j] >> 16)) * scale * wv[2 * j + 1];
+      hv[j] = pack_h2(lo, hi);
+    }
+    *reinterpret_cast<u32x4*>(next.h + t * H + h) = hv;
+    float g = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      g = fmaf(h2f((uint16_t)(ng[j] & 0xffffu)), h2f((uint16_t)(hv[j] & 0xffffu)), g);
+      g = fmaf(h2f((uint16_t)(ng[j] >> 16)), h2f((uint16_t)(hv[j] >> 16)), g);
+    }
+    const double gd = block_sum_256(g, red);
+    if (threadIdx.x == 0) {
+      next.sigma[t] = (float)(gd >= 0.0 ? 1.0 / (1.0 + exp(-gd)) : exp(gd) / (1.0 + exp(gd)));
+    }
+  }
+}
+
 
 // ---------------------------------------------------------------------------
 // host
@@ -847,9 +944,15 @@ static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint1
   }
   rc = launch_check("grouped down GEMM");
   if (rc != AIMA_OK) return rc;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)d.T), dim3(256), 0, st, w.contrib,
-                     w.inverse_map, d.k, d.A, x, L.shared_gate_vec, sigma_in, residual,
-                     (int64_t)d.H, out, next);
+  if (d.H == 2048 && d.k <= 8) {
+    hipLaunchKernelGGL(combine2048_kernel, dim3((unsigned)d.T), dim3(256), 0, st, w.contrib,
+                       w.inverse_map, d.k, d.A, x, L.shared_gate_vec, sigma_in, residual, out,
+                       next);
+  } else {
+    hipLaunchKernelGGL(combine_kernel, dim3((unsigned)d.T), dim3(256), 0, st, w.contrib,
+                       w.inverse_map, d.k, d.A, x, L.shared_gate_vec, sigma_in, residual,
+                       (int64_t)d.H, out, next);
+  }
   return launch_check("grouped combine");
 }
 
