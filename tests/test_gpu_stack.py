@@ -213,6 +213,25 @@ def test_decode_plan_small_stack(pkg, dev):
         assert_parity(f16_to_f32(a), oracle.f16_values(ref[0]), what=f"plan small rep={rep}")
 
 
+@pytest.mark.parametrize("k", [1, 4])
+def test_decode_plan_small_k(pkg, dev, k):
+    """Fewer than 8 routed experts: the XCDs of the missing ranks compute only
+    their shared-expert slice (2 layers of the real width vs the oracle)."""
+    layers = make_stack(pkg, dev, 2, 2048, 512, 16, seed=1200 + k)
+    lnp = [moe_to_oracle(l) for l in layers]
+    norms = [l.norm_weight.cpu().numpy() for l in layers]
+    plan = pkg.DecodePlan(layers, k=k)
+    x = pkg.synth.activations(1, 2048, 95 + k, dev)
+    logits = torch.stack([pkg.synth.router_logits(1, 16, 96 + k + l, dev)[0] for l in range(2)])
+    ids, w = pkg.select_router_topk(logits, k)
+    out = plan.run(x[0], router_logits=logits)
+    torch.cuda.synchronize()
+    assert plan.error_bits() == 0
+    ref = oracle_stack(lnp, norms, f16_bits(x), ids.cpu().numpy()[:, None],
+                       w.cpu().numpy()[:, None])
+    assert_parity(f16_to_f32(out), oracle.f16_values(ref[0]), what=f"plan k={k}")
+
+
 @pytest.mark.parametrize("group", [64, 256])
 def test_decode_plan_other_groups(pkg, dev, group):
     """Group sizes other than 128 run the general kernel instance (per-row
