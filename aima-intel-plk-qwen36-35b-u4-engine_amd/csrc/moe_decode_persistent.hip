@@ -77,6 +77,7 @@ constexpr int kMaxK = 8;
 constexpr uint32_t kSpinLimit = 1u << 22;
 constexpr int kMaxLayers = 79;
 static_assert(kPairs % 3 == 0, "blocks own whole act records");
+static_assert(kActRecords <= 192, "the activation poll covers records 0..191");
 static_assert(kRowsB % kWaves == 0 && kWaveRowsB == 8, "8 output rows per wave");
 
 struct PersistArgs {
