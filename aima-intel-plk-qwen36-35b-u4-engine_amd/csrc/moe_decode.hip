@@ -5,7 +5,8 @@
 // (4 rows of H/2 bytes) with 128-bit loads, reduces each row across its lane
 // segment and applies silu(gate)*up in registers; the activation is stored as
 // f16 [k+1][I].  Block 0 also evaluates the shared expert's scalar gate
-// sigmoid(gate_vec . h).
+// sigmoid(gate_vec . h), with all its threads (row_dot_f16: one wave alone
+// made block 0 the last to finish).
 //
 // Phase B (down + aggregate + residual): each block owns 8 output rows.  Its
 // four waves split the k+1 down matrices (slot s -> wave s % 4), each lane
@@ -186,12 +187,10 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
       act[pair] = f2h(silu_mul(g, u));
     }
   }
-  if (blockIdx.x == 0 && wave == 0) {
-    float acc = 0.f;
-    for (int64_t i = lane; i < L.hidden; i += 64) acc += h2f(L.shared_gate_vec[i]) * h2f(x[i]);
-    acc = segment_sum<64>(acc);
-    if (lane == 0) {
-      const double t = acc;
+  if (blockIdx.x == 0) {
+    __shared__ float red[4];
+    const double t = row_dot_f16(L.shared_gate_vec, x, L.hidden, red);
+    if (threadIdx.x == 0) {
       const double r = t >= 0.0 ? 1.0 / (1.0 + exp(-t)) : exp(t) / (1.0 + exp(t));
       *sigma = (float)r;
     }
