@@ -9,9 +9,10 @@
 // made block 0 the last to finish).
 //
 // Phase B (down + aggregate + residual): each block owns 8 output rows.  Its
-// four waves split the k+1 down matrices (slot s -> wave s % 4), each lane
-// accumulates w_s * (row . act_s) over its slots, and the four partial sums
-// plus the residual are added in a fixed order: no atomics, deterministic.
+// eight waves split the k+1 down matrices (slot s -> wave s % 8) and issue
+// all their weight loads before any compute; each lane accumulates
+// w_s * (row . act_s) over its slots, and the eight partial sums plus the
+// residual are added in a fixed order: no atomics, deterministic.
 #include "common.h"
 
 #include <math.h>
@@ -20,6 +21,8 @@ namespace aima {
 
 constexpr int kPairsPerWave = 2;
 constexpr int kDownRowsPerBlock = 8;
+constexpr int kDownThreads = 512;      // 8 waves, wave w owns slots w, w + 8, w + 16
+constexpr int kDownSlotsPerWave = 3;   // slots per wave per batch of 24
 
 struct DecodeWs {
   uint32_t* err;
@@ -96,68 +99,88 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
   using G = Geom<KCH>;
   constexpr int NR = 2 * kPairsPerWave;          // rows per wave
   constexpr int PASSES = (NR + G::RPI - 1) / G::RPI;
+  constexpr int BP = 4 * kPairsPerWave;          // pairs per block (one slot, consecutive)
+  constexpr int kMaxGroups = G::K / 32;
+  // the block's scales and zero points: gate rows j0.. and up rows I+j0..,
+  // each a contiguous run, staged through LDS (one element per thread)
+  __shared__ uint16_t s_lds[2 * BP * kMaxGroups];
+  __shared__ uint8_t z_lds[2][BP * kMaxGroups / 2];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int seg = lane / G::SEG;
   const int cl = lane % G::SEG;
   const int64_t I = L.inter;
-  const int64_t groups = G::K / L.group;
+  const int groups = G::K / L.group;
   const int64_t total_pairs = (int64_t)(k + 1) * I;
-  const int64_t pair0 = ((int64_t)blockIdx.x * 4 + wave) * kPairsPerWave;
+  const int64_t bpair0 = (int64_t)blockIdx.x * BP;
+  const int64_t pair0 = bpair0 + wave * kPairsPerWave;
   const uint32_t magic = u4_magic();
 
+  // the block's slot (inter is a multiple of BP: every block lies in one slot)
+  const int64_t slot = bpair0 / I;
+  const int64_t j0 = bpair0 - slot * I;
+  const int64_t rows_e = 2 * I;
+  const uint8_t* qw;
+  const uint16_t* sc;
+  const uint8_t* zp;
+  bool valid = bpair0 < total_pairs;
+  if (slot < k) {
+    const int32_t e = valid ? ids[slot] : 0;
+    if (valid && (e < 0 || e >= L.experts)) {
+      if (j0 == 0 && threadIdx.x == 0) atomicOr(err, AIMA_DEVERR_EXPERT_RANGE);
+      valid = false;
+    }
+    const int64_t ee = valid ? e : 0;
+    qw = L.gate_up.qweight + ee * rows_e * (G::K / 2);
+    sc = L.gate_up.scale + ee * rows_e * groups;
+    zp = L.gate_up.zp + ee * (rows_e * groups / 2);
+  } else {
+    qw = L.shared_gate_up.qweight;
+    sc = L.shared_gate_up.scale;
+    zp = L.shared_gate_up.zp;
+  }
+  // weights first: they stream while the activation operands are built
+  u32x4 w[PASSES][G::NC];
+#pragma unroll
+  for (int ps = 0; ps < PASSES; ++ps) {
+    const int ri = ps * G::RPI + seg;  // row index in this wave's list
+    const int64_t row = ((ri & 1) ? I : 0) + j0 + wave * kPairsPerWave + ri / 2;
+#pragma unroll
+    for (int i = 0; i < G::NC; ++i) {
+      const int c = cl + i * G::SEG;
+      w[ps][i] = (valid && ri < NR) ? load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16)
+                                    : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  if (valid) {
+    const int n = BP * groups;  // scales per run
+    for (int t = threadIdx.x; t < 2 * n; t += 256) {
+      const int up = t >= n;
+      s_lds[t] = sc[((up ? I : 0) + j0) * groups + (t - up * n)];
+    }
+    for (int t = threadIdx.x; t < n; t += 256) {
+      const int up = t >= n / 2;
+      z_lds[up][t - up * (n / 2)] = zp[(((up ? I : 0) + j0) * groups >> 1) + (t - up * (n / 2))];
+    }
+  }
   XChunk xc[G::NC];
   load_chunks<KCH>(x, cl, xc);
-
-  u32x4 w[PASSES][G::NC];
+  __syncthreads();
   float s[PASSES][G::NC];
   uint32_t z[PASSES][G::NC];
   bool ok[PASSES];
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
-    const int ri = ps * G::RPI + seg;  // row index in this wave's list
-    const int64_t pair = pair0 + ri / 2;
-    const bool up = ri & 1;
-    bool valid = ri < NR && pair < total_pairs;
-    const uint8_t* qw = nullptr;
-    const uint16_t* sc = nullptr;
-    const uint8_t* zp = nullptr;
-    int64_t row = 0;
-    if (valid) {
-      const int64_t slot = pair / I;
-      const int64_t j = pair - slot * I;
-      row = (up ? I : 0) + j;
-      const int64_t rows_e = 2 * I;
-      if (slot < k) {
-        const int32_t e = ids[slot];
-        if (e < 0 || e >= L.experts) {
-          if (j == 0 && !up && cl == 0) atomicOr(err, AIMA_DEVERR_EXPERT_RANGE);
-          valid = false;
-        } else {
-          qw = L.gate_up.qweight + (int64_t)e * rows_e * (G::K / 2);
-          sc = L.gate_up.scale + (int64_t)e * rows_e * groups;
-          zp = L.gate_up.zp + (int64_t)e * (rows_e * groups / 2);
-        }
-      } else {
-        qw = L.shared_gate_up.qweight;
-        sc = L.shared_gate_up.scale;
-        zp = L.shared_gate_up.zp;
-      }
-    }
-    ok[ps] = valid;
+    const int ri = ps * G::RPI + seg;
+    const int up = ri & 1;
+    const int lr = wave * kPairsPerWave + ri / 2;  // row within the block's run
+    ok[ps] = valid && ri < NR;
 #pragma unroll
     for (int i = 0; i < G::NC; ++i) {
       const int c = cl + i * G::SEG;
-      if (valid) {
-        w[ps][i] = load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16);
-        const int64_t gi = row * groups + ((int64_t)c * 32) / L.group;
-        s[ps][i] = h2f(sc[gi]);
-        z[ps][i] = u4_code(zp, gi);
-      } else {
-        w[ps][i] = u32x4{0u, 0u, 0u, 0u};
-        s[ps][i] = 0.f;
-        z[ps][i] = 0u;
-      }
+      const int gi = lr * groups + ((c * 32) / L.group);
+      s[ps][i] = ok[ps] ? h2f(s_lds[up * BP * groups + gi]) : 0.f;
+      z[ps][i] = ok[ps] ? (uint32_t)(z_lds[up][gi >> 1] >> ((gi & 1) * 4)) & 0xfu : 0u;
     }
   }
   float v[PASSES];
@@ -175,7 +198,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
   for (int ri = 0; ri < NR; ++ri) rows[ri] = __shfl(v[ri / G::RPI], (ri % G::RPI) * G::SEG, 64);
   if (lane < kPairsPerWave) {
     const int64_t pair = pair0 + lane;
-    if (pair < total_pairs) {
+    if (valid && pair < total_pairs) {
       float g = 0.f, u = 0.f;
 #pragma unroll
       for (int p = 0; p < kPairsPerWave; ++p) {
@@ -201,13 +224,14 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
 // phase B
 // ---------------------------------------------------------------------------
 template <int KCH>
-__global__ __launch_bounds__(256) void decode_down_kernel(
+__global__ __launch_bounds__(kDownThreads) void decode_down_kernel(
     aima_moe_layer L, const int32_t* __restrict__ ids, const float* __restrict__ rw, int k,
     const uint16_t* __restrict__ act, const float* __restrict__ sigma,
     const uint16_t* __restrict__ residual, uint16_t* __restrict__ out) {
   using G = Geom<KCH>;
   constexpr int PASSES = (kDownRowsPerBlock + G::RPI - 1) / G::RPI;
-  __shared__ float part[4][PASSES * G::RPI];
+  constexpr int NW = kDownThreads / 64;
+  __shared__ float part[NW][PASSES * G::RPI];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int seg = lane / G::SEG;
@@ -221,54 +245,68 @@ __global__ __launch_bounds__(256) void decode_down_kernel(
   float acc[PASSES];
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) acc[ps] = 0.f;
-
-  for (int slot = wave; slot <= k; slot += 4) {
-    const uint8_t* qw;
-    const uint16_t* sc;
-    const uint8_t* zp;
-    float coef;
-    if (slot < k) {
-      const int32_t e = ids[slot];
-      if (e < 0 || e >= L.experts) continue;  // flagged by phase A
-      qw = L.down.qweight + (int64_t)e * H * (G::K / 2);
-      sc = L.down.scale + (int64_t)e * H * groups;
-      zp = L.down.zp + (int64_t)e * (H * groups / 2);
-      coef = rw[slot];
-    } else {
-      qw = L.shared_down.qweight;
-      sc = L.shared_down.scale;
-      zp = L.shared_down.zp;
-      coef = *sigma;
-    }
-    u32x4 w[PASSES][G::NC];
-    float s[PASSES][G::NC];
-    uint32_t z[PASSES][G::NC];
+  // in each batch of NW * kDownSlotsPerWave slots, wave w owns slots
+  // base + w + q NW (<= k) and issues all their weight loads before any
+  // compute; k + 1 <= 24 takes one batch
+  for (int base = 0; base <= k; base += NW * kDownSlotsPerWave) {
+    u32x4 w[kDownSlotsPerWave][PASSES][G::NC];
+    float s[kDownSlotsPerWave][PASSES][G::NC];
+    uint32_t z[kDownSlotsPerWave][PASSES][G::NC];
+    float coef[kDownSlotsPerWave];
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      const int64_t row = h0 + ps * G::RPI + seg;
-#pragma unroll
-      for (int i = 0; i < G::NC; ++i) {
-        const int c = cl + i * G::SEG;
-        if (ps * G::RPI + seg < kDownRowsPerBlock && row < H) {
-          w[ps][i] = load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16);
-          const int64_t gi = row * groups + ((int64_t)c * 32) / L.group;
-          s[ps][i] = h2f(sc[gi]);
-          z[ps][i] = u4_code(zp, gi);
+    for (int q = 0; q < kDownSlotsPerWave; ++q) {
+      const int slot = base + wave + q * NW;
+      const uint8_t* qw = L.shared_down.qweight;
+      const uint16_t* sc = L.shared_down.scale;
+      const uint8_t* zp = L.shared_down.zp;
+      bool live = slot <= k;
+      coef[q] = 0.f;
+      if (live && slot < k) {
+        const int32_t e = ids[slot];
+        if (e < 0 || e >= L.experts) {
+          live = false;  // flagged by phase A
         } else {
-          w[ps][i] = u32x4{0u, 0u, 0u, 0u};
-          s[ps][i] = 0.f;
-          z[ps][i] = 0u;
+          qw = L.down.qweight + (int64_t)e * H * (G::K / 2);
+          sc = L.down.scale + (int64_t)e * H * groups;
+          zp = L.down.zp + (int64_t)e * (H * groups / 2);
+          coef[q] = rw[slot];
+        }
+      } else if (live) {
+        coef[q] = *sigma;
+      }
+#pragma unroll
+      for (int ps = 0; ps < PASSES; ++ps) {
+        const int64_t row = h0 + ps * G::RPI + seg;
+#pragma unroll
+        for (int i = 0; i < G::NC; ++i) {
+          const int c = cl + i * G::SEG;
+          if (live && ps * G::RPI + seg < kDownRowsPerBlock && row < H) {
+            w[q][ps][i] = load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16);
+            const int64_t gi = row * groups + ((int64_t)c * 32) / L.group;
+            s[q][ps][i] = h2f(sc[gi]);
+            z[q][ps][i] = u4_code(zp, gi);
+          } else {
+            w[q][ps][i] = u32x4{0u, 0u, 0u, 0u};
+            s[q][ps][i] = 0.f;
+            z[q][ps][i] = 0u;
+          }
         }
       }
     }
-    XChunk xc[G::NC];
-    load_chunks<KCH>(act + (int64_t)slot * I, cl, xc);
 #pragma unroll
-    for (int ps = 0; ps < PASSES; ++ps) {
-      float d = 0.f;
+    for (int q = 0; q < kDownSlotsPerWave; ++q) {
+      const int slot = base + wave + q * NW;
+      if (slot > k) break;
+      XChunk xc[G::NC];
+      load_chunks<KCH>(act + (int64_t)slot * I, cl, xc);
 #pragma unroll
-      for (int i = 0; i < G::NC; ++i) d += u4_chunk_dot(w[ps][i], xc[i], z[ps][i], s[ps][i], magic);
-      acc[ps] += coef * d;
+      for (int ps = 0; ps < PASSES; ++ps) {
+        float d = 0.f;
+#pragma unroll
+        for (int i = 0; i < G::NC; ++i)
+          d += u4_chunk_dot(w[q][ps][i], xc[i], z[q][ps][i], s[q][ps][i], magic);
+        acc[ps] += coef[q] * d;
+      }
     }
   }
 #pragma unroll
@@ -280,8 +318,9 @@ __global__ __launch_bounds__(256) void decode_down_kernel(
   if (threadIdx.x < kDownRowsPerBlock) {
     const int64_t row = h0 + threadIdx.x;
     if (row < H) {
-      const float f = ((part[0][threadIdx.x] + part[1][threadIdx.x]) + part[2][threadIdx.x]) +
-                      part[3][threadIdx.x];
+      float f = part[0][threadIdx.x];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) f += part[ww][threadIdx.x];
       const float r = residual ? h2f(residual[row]) : 0.f;
       out[row] = f2h(r + f);
     }
@@ -335,8 +374,8 @@ static void launch_down(const aima_moe_layer& L, const int32_t* ids, const float
                         const DecodeWs& w, const uint16_t* residual, uint16_t* out,
                         hipStream_t st) {
   const int64_t blocks = (L.hidden + kDownRowsPerBlock - 1) / kDownRowsPerBlock;
-  hipLaunchKernelGGL((decode_down_kernel<KCH>), dim3((unsigned)blocks), dim3(256), 0, st, L, ids,
-                     rw, k, w.act, w.sigma, residual, out);
+  hipLaunchKernelGGL((decode_down_kernel<KCH>), dim3((unsigned)blocks), dim3(kDownThreads), 0, st, L,
+                     ids, rw, k, w.act, w.sigma, residual, out);
 }
 
 static int decode_layer(const aima_moe_layer& L, const uint16_t* x, const uint16_t* residual,

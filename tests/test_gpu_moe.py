@@ -61,6 +61,24 @@ def test_decode_small_topk(pkg, dev, layer_small, k):
     assert_parity(got, ref, what=f"small k={k}")
 
 
+@pytest.mark.parametrize("k", [23, 24, 40])
+def test_decode_wide_topk(pkg, dev, k):
+    """k + 1 > 24 slots: the down phase takes its slots in several batches."""
+    layer = pkg.synth.moe_layer(hidden=512, inter=128, experts=40, seed=23, device=dev)
+    g = np.random.default_rng(50 + k)
+    ids = g.permutation(40)[:k].astype(np.int32)[None]  # router top-k stops at 16
+    w = g.random(k).astype(np.float32)
+    w = (w / w.sum())[None]
+    x = pkg.synth.activations(1, 512, 51 + k, dev)[0]
+    res = pkg.synth.activations(1, 512, 52 + k, dev)[0]
+    out = pkg.run_moe_ffn_layer(layer, x, torch.from_numpy(ids[0]).to(dev),
+                                torch.from_numpy(w[0]).to(dev), residual=res)
+    torch.cuda.synchronize()
+    ref = oracle.moe_ffn_tokens(moe_to_oracle(layer), f16_to_f32(x)[None], ids, w,
+                                residual=f16_to_f32(res)[None], threads=1)
+    assert_parity(f16_to_f32(out), ref[0], what=f"wide k={k}")
+
+
 def test_decode_flags_bad_expert_id(pkg, dev, layer_small):
     layer, _ = layer_small
     ws = pkg.Workspace(dev)
