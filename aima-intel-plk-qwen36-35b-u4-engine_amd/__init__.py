@@ -18,10 +18,12 @@ from .ops import (  # noqa: F401
     build_grouped_schedule,
     grouped_moe_prefill,
     matvec_u4,
+    matvec_u4_multi,
     moe_decode_down,
     moe_decode_gate_up,
     moe_stack_decode,
     moe_stack_prefill,
+    router_fc_topk,
     run_moe_ffn_layer,
     select_router_topk,
     u4_dequant,

@@ -27,6 +27,7 @@ AIMA_DEVERR_EXPERT_DUPLICATE = 2
 AIMA_DEVERR_TIMEOUT = 4
 AIMA_OUT_F16 = 0
 AIMA_OUT_F32 = 1
+AIMA_MAX_MULTI_OUT = 4
 
 # Every symbol the header declares, with (restype, argtypes).
 _vp = C.c_void_p
@@ -56,6 +57,10 @@ SIGNATURES = {
     "aima_u4_matvec": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _vp]),
     "aima_rmsnorm": (C.c_int, [_vp, _vp, _i64, _i64, _f32, _vp, _vp]),
     "aima_router_topk": (C.c_int, [_vp, _i64, _i32, _i32, _f32, _vp, _vp, _vp]),
+    "aima_u4_matvec_multi": (C.c_int, [_vp, _i32, C.POINTER(U4TensorC), C.POINTER(_i64), _i64,
+                                       _i32, C.POINTER(_vp), C.POINTER(_i32), _vp]),
+    "aima_router_fc_topk": (C.c_int, [_vp, C.POINTER(U4TensorC), _i32, _i64, _i32, _i32, _f32,
+                                      _vp, _vp, _vp, _vp]),
     "aima_moe_decode_workspace_size": (C.c_int, [_LP, _i32, _szp]),
     "aima_moe_ffn_decode": (C.c_int, [_LP, _vp, _vp, _vp, _vp, _i32, _vp, _vp, C.c_size_t,
                                       _vp]),

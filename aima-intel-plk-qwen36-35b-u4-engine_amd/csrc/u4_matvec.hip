@@ -71,11 +71,12 @@ __device__ __forceinline__ void load_x_chunks(const uint16_t* __restrict__ x,
   }
 }
 
+// Rows blk * BR .. +BR of one matrix (the body of every matvec block).
 template <int KCH, int RG>
-__global__ __launch_bounds__(256) void u4_matvec_kernel(
+__device__ __forceinline__ void matvec_block(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ qw,
     const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zp,
-    int64_t n, int group_log2, void* __restrict__ y, int out_f32) {
+    int64_t n, int group_log2, void* __restrict__ y, int out_f32, int64_t blk) {
   using G = RowGeom<KCH>;
   constexpr int BR = 4 * RG * G::RPI;       // rows of the block (consecutive)
   constexpr int kMaxGroups = G::K / 32;     // groups per row at group 32
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(256) void u4_matvec_kernel(
   const int groups = G::K >> group_log2;
   const uint32_t magic = u4_magic();
 
-  const int64_t brow0 = (int64_t)blockIdx.x * BR;
+  const int64_t brow0 = blk * BR;
   const int64_t row0 = brow0 + (int64_t)wave * (RG * G::RPI);
   u32x4 w[RG][G::NC];
 #pragma unroll
@@ -135,6 +136,42 @@ __global__ __launch_bounds__(256) void u4_matvec_kernel(
       }
     }
   }
+}
+
+template <int KCH, int RG>
+__global__ __launch_bounds__(256) void u4_matvec_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ qw,
+    const uint16_t* __restrict__ scale, const uint8_t* __restrict__ zp,
+    int64_t n, int group_log2, void* __restrict__ y, int out_f32) {
+  matvec_block<KCH, RG>(x, qw, scale, zp, n, group_log2, y, out_f32, blockIdx.x);
+}
+
+constexpr int kMaxMultiOut = AIMA_MAX_MULTI_OUT;
+
+// Several matrices over one input x (the reference's multi-output fixed FC):
+// block b belongs to the matrix whose block range holds it, so the pointer
+// selection is uniform per block.
+struct MultiMatvec {
+  const uint8_t* qw[kMaxMultiOut];
+  const uint16_t* scale[kMaxMultiOut];
+  const uint8_t* zp[kMaxMultiOut];
+  void* y[kMaxMultiOut];
+  int64_t n[kMaxMultiOut];
+  int32_t out_f32[kMaxMultiOut];
+  int32_t first_block[kMaxMultiOut + 1];
+  int32_t count;
+};
+
+template <int KCH, int RG>
+__global__ __launch_bounds__(256) void u4_matvec_multi_kernel(const uint16_t* __restrict__ x,
+                                                              MultiMatvec m, int group_log2) {
+  const int b = blockIdx.x;
+  int j = 0;
+#pragma unroll
+  for (int t = 1; t < kMaxMultiOut; ++t)
+    if (t < m.count && b >= m.first_block[t]) j = t;
+  matvec_block<KCH, RG>(x, m.qw[j], m.scale[j], m.zp[j], m.n[j], group_log2, m.y[j],
+                        m.out_f32[j], b - m.first_block[j]);
 }
 
 template <int KCH>
@@ -183,6 +220,9 @@ int rmsnorm_launch(const uint16_t* x, const float* weight, int64_t rows, int64_t
 // ---------------------------------------------------------------------------
 constexpr int kRouterMaxPerLane = 16;  // experts <= 1024
 
+// PER = logits per lane (experts <= 64 PER); lane r keeps the rank-r pick in
+// registers, and lane 0 sums the picks in rank order through shuffles.
+template <int PER>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, int64_t tokens, int experts, int k,
     float min_weight_sum, int32_t* __restrict__ ids, float* __restrict__ weights) {
@@ -190,40 +230,39 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   const int64_t token = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (token >= tokens) return;
   const float* l = logits + token * experts;
-  const int per = (experts + 63) / 64;
-  float v[kRouterMaxPerLane];
+  float v[PER];
   float mx = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kRouterMaxPerLane; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int i = lane + 64 * j;
-    v[j] = (j < per && i < experts) ? l[i] : -INFINITY;
+    v[j] = i < experts ? l[i] : -INFINITY;
     mx = fmaxf(mx, v[j]);
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  double e[kRouterMaxPerLane];
+  double e[PER];
   double sum = 0.0;
 #pragma unroll
-  for (int j = 0; j < kRouterMaxPerLane; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int i = lane + 64 * j;
-    e[j] = (j < per && i < experts) ? exp((double)v[j] - (double)mx) : 0.0;
+    e[j] = i < experts ? exp((double)v[j] - (double)mx) : 0.0;
     sum += e[j];
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-  float p[kRouterMaxPerLane];
+  float p[PER];
 #pragma unroll
-  for (int j = 0; j < kRouterMaxPerLane; ++j) {
+  for (int j = 0; j < PER; ++j) {
     const int i = lane + 64 * j;
-    p[j] = (j < per && i < experts) ? (float)(e[j] / sum) : -INFINITY;
+    p[j] = i < experts ? (float)(e[j] / sum) : -INFINITY;
   }
-  float sel_p[16];
-  int sel_i[16];
+  float my_p = 0.f;
+  int my_i = 0;
   for (int r = 0; r < k; ++r) {
     float bp = -INFINITY;
     int bi = 0x7fffffff;
 #pragma unroll
-    for (int j = 0; j < kRouterMaxPerLane; ++j) {
+    for (int j = 0; j < PER; ++j) {
       const int i = lane + 64 * j;
       if (i < experts && (p[j] > bp || (p[j] == bp && i < bi))) {
         bp = p[j];
@@ -239,21 +278,44 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
         bi = oi;
       }
     }
-    sel_p[r] = bp;
-    sel_i[r] = bi;
+    if (lane == r) {
+      my_p = bp;
+      my_i = bi;
+    }
 #pragma unroll
-    for (int j = 0; j < kRouterMaxPerLane; ++j) {
+    for (int j = 0; j < PER; ++j) {
       if (lane + 64 * j == bi) p[j] = -INFINITY;
     }
   }
-  if (lane == 0) {
-    float s = 0.f;
-    for (int r = 0; r < k; ++r) s += sel_p[r];
-    const float den = s > min_weight_sum ? s : min_weight_sum;
-    for (int r = 0; r < k; ++r) {
-      ids[token * k + r] = sel_i[r];
-      weights[token * k + r] = sel_p[r] / den;
-    }
+  float s = 0.f;
+  for (int r = 0; r < k; ++r) s += __shfl(my_p, r, 64);
+  const float den = s > min_weight_sum ? s : min_weight_sum;
+  if (lane < k) {
+    ids[token * k + lane] = my_i;
+    weights[token * k + lane] = my_p / den;
+  }
+}
+
+static void launch_router_topk(const float* logits, int64_t tokens, int experts, int k,
+                               float min_weight_sum, int32_t* ids, float* weights,
+                               hipStream_t st) {
+  const unsigned blocks = (unsigned)((tokens + 3) / 4);
+  const int per = (experts + 63) / 64;
+  if (per <= 1) {
+    hipLaunchKernelGGL(router_topk_kernel<1>, dim3(blocks), dim3(256), 0, st, logits, tokens,
+                       experts, k, min_weight_sum, ids, weights);
+  } else if (per <= 2) {
+    hipLaunchKernelGGL(router_topk_kernel<2>, dim3(blocks), dim3(256), 0, st, logits, tokens,
+                       experts, k, min_weight_sum, ids, weights);
+  } else if (per <= 4) {
+    hipLaunchKernelGGL(router_topk_kernel<4>, dim3(blocks), dim3(256), 0, st, logits, tokens,
+                       experts, k, min_weight_sum, ids, weights);
+  } else if (per <= 8) {
+    hipLaunchKernelGGL(router_topk_kernel<8>, dim3(blocks), dim3(256), 0, st, logits, tokens,
+                       experts, k, min_weight_sum, ids, weights);
+  } else {
+    hipLaunchKernelGGL(router_topk_kernel<kRouterMaxPerLane>, dim3(blocks), dim3(256), 0, st,
+                       logits, tokens, experts, k, min_weight_sum, ids, weights);
   }
 }
 
@@ -272,6 +334,46 @@ int u4_matvec_dispatch(const uint16_t* x, const uint8_t* qw, const uint16_t* sca
       return fail(AIMA_E_UNSUPPORTED, "u4_matvec: K must be a power of two in [128, 8192]");
   }
   return launch_check("u4_matvec");
+}
+
+template <int KCH>
+static void launch_matvec_multi(const uint16_t* x, MultiMatvec m, int glog2, hipStream_t st) {
+  // the single-matrix rule (8 row passes per wave once that still leaves
+  // two blocks per CU) applied to the summed block count
+  const int64_t rows8 = 4 * 8 * RowGeom<KCH>::RPI;
+  int64_t blocks8 = 0;
+  for (int j = 0; j < m.count; ++j) blocks8 += (m.n[j] + rows8 - 1) / rows8;
+  const int rg = blocks8 >= 512 ? 8 : 4;
+  const int64_t br = 4 * rg * RowGeom<KCH>::RPI;
+  int64_t b = 0;
+  for (int j = 0; j < m.count; ++j) {
+    m.first_block[j] = (int32_t)b;
+    b += (m.n[j] + br - 1) / br;
+  }
+  m.first_block[m.count] = (int32_t)b;
+  if (rg == 8) {
+    hipLaunchKernelGGL((u4_matvec_multi_kernel<KCH, 8>), dim3((unsigned)b), dim3(256), 0, st, x, m,
+                       glog2);
+  } else {
+    hipLaunchKernelGGL((u4_matvec_multi_kernel<KCH, 4>), dim3((unsigned)b), dim3(256), 0, st, x, m,
+                       glog2);
+  }
+}
+
+static int u4_matvec_multi_dispatch(const uint16_t* x, const MultiMatvec& m, int64_t k, int glog2,
+                                    hipStream_t st) {
+  switch (k) {
+    case 128: launch_matvec_multi<4>(x, m, glog2, st); break;
+    case 256: launch_matvec_multi<8>(x, m, glog2, st); break;
+    case 512: launch_matvec_multi<16>(x, m, glog2, st); break;
+    case 1024: launch_matvec_multi<32>(x, m, glog2, st); break;
+    case 2048: launch_matvec_multi<64>(x, m, glog2, st); break;
+    case 4096: launch_matvec_multi<128>(x, m, glog2, st); break;
+    case 8192: launch_matvec_multi<256>(x, m, glog2, st); break;
+    default:
+      return fail(AIMA_E_UNSUPPORTED, "u4_matvec_multi: K must be a power of two in [128, 8192]");
+  }
+  return launch_check("u4_matvec_multi");
 }
 
 int group_log2_of(int group) {
@@ -321,6 +423,39 @@ extern "C" int aima_u4_matvec(const uint16_t* x, const uint8_t* qweight,
                             (hipStream_t)stream);
 }
 
+extern "C" int aima_u4_matvec_multi(const uint16_t* x, int32_t count,
+                                    const aima_u4_tensor* weights, const int64_t* n, int64_t k,
+                                    int32_t group, void* const* y, const int32_t* out_dtype,
+                                    void* stream) {
+  AIMA_REQUIRE(x && weights && n && y && out_dtype, "u4_matvec_multi: null pointer");
+  AIMA_REQUIRE(count >= 1 && count <= kMaxMultiOut,
+               "u4_matvec_multi: count must be in [1, AIMA_MAX_MULTI_OUT]");
+  const int glog2 = group_log2_of(group);
+  AIMA_REQUIRE(glog2 > 0, "u4_matvec_multi: group must be 32, 64, 128 or 256");
+  AIMA_REQUIRE(k % group == 0, "u4_matvec_multi: k must be a multiple of group");
+  AIMA_REQUIRE(aligned(x, 16), "u4_matvec_multi: x must be 16-byte aligned");
+  MultiMatvec m{};
+  m.count = count;
+  int64_t rows = 0;
+  for (int j = 0; j < count; ++j) {
+    const aima_u4_tensor& w = weights[j];
+    AIMA_REQUIRE(w.qweight && w.scale && w.zp && y[j], "u4_matvec_multi: null output or tensor");
+    AIMA_REQUIRE(aligned(w.qweight, 16), "u4_matvec_multi: qweight must be 16-byte aligned");
+    AIMA_REQUIRE(n[j] > 0, "u4_matvec_multi: every n must be positive");
+    AIMA_REQUIRE(out_dtype[j] == AIMA_OUT_F16 || out_dtype[j] == AIMA_OUT_F32,
+                 "u4_matvec_multi: out_dtype must be AIMA_OUT_F16 or AIMA_OUT_F32");
+    m.qw[j] = w.qweight;
+    m.scale[j] = w.scale;
+    m.zp[j] = w.zp;
+    m.y[j] = y[j];
+    m.n[j] = n[j];
+    m.out_f32[j] = out_dtype[j] == AIMA_OUT_F32;
+    rows += n[j];
+  }
+  AIMA_REQUIRE(rows < ((int64_t)1 << 31), "u4_matvec_multi: too many rows");
+  return u4_matvec_multi_dispatch(x, m, k, glog2, (hipStream_t)stream);
+}
+
 extern "C" int aima_rmsnorm(const uint16_t* x, const float* weight, int64_t rows,
                             int64_t hidden, float eps, uint16_t* out, void* stream) {
   AIMA_REQUIRE(x && weight && out, "rmsnorm: null pointer");
@@ -338,9 +473,32 @@ extern "C" int aima_router_topk(const float* logits, int64_t tokens, int32_t exp
                "router_topk: experts must be in [1, 1024]");
   AIMA_REQUIRE(k > 0 && k <= 16 && k <= experts, "router_topk: k must be in [1, min(16, experts)]");
   AIMA_REQUIRE(min_weight_sum > 0.f, "router_topk: minimum weight sum must be positive");
-  const int64_t blocks = (tokens + 3) / 4;
-  hipLaunchKernelGGL(router_topk_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     (hipStream_t)stream, logits, tokens, experts, k, min_weight_sum, ids,
-                     weights);
+  launch_router_topk(logits, tokens, experts, k, min_weight_sum, ids, weights,
+                     (hipStream_t)stream);
   return launch_check("router_topk");
+}
+
+extern "C" int aima_router_fc_topk(const uint16_t* h, const aima_u4_tensor* router,
+                                   int32_t experts, int64_t hidden, int32_t group, int32_t k,
+                                   float min_weight_sum, float* logits, int32_t* ids,
+                                   float* weights, void* stream) {
+  AIMA_REQUIRE(h && router && router->qweight && router->scale && router->zp && logits && ids &&
+                   weights,
+               "router_fc_topk: null pointer");
+  AIMA_REQUIRE(experts > 0 && experts <= 64 * kRouterMaxPerLane,
+               "router_fc_topk: experts must be in [1, 1024]");
+  AIMA_REQUIRE(k > 0 && k <= 16 && k <= experts,
+               "router_fc_topk: k must be in [1, min(16, experts)]");
+  AIMA_REQUIRE(min_weight_sum > 0.f, "router_fc_topk: minimum weight sum must be positive");
+  const int glog2 = group_log2_of(group);
+  AIMA_REQUIRE(glog2 > 0, "router_fc_topk: group must be 32, 64, 128 or 256");
+  AIMA_REQUIRE(hidden % group == 0, "router_fc_topk: hidden must be a multiple of group");
+  AIMA_REQUIRE(aligned(router->qweight, 16) && aligned(h, 16),
+               "router_fc_topk: qweight and h must be 16-byte aligned");
+  const hipStream_t st = (hipStream_t)stream;
+  const int rc = u4_matvec_dispatch(h, router->qweight, router->scale, router->zp, experts,
+                                    hidden, glog2, logits, 1, st);
+  if (rc != AIMA_OK) return rc;
+  launch_router_topk(logits, 1, experts, k, min_weight_sum, ids, weights, st);
+  return launch_check("router_fc_topk");
 }

@@ -119,6 +119,56 @@ def matvec_u4(x: torch.Tensor, w: U4Weight, out_dtype=torch.float16) -> torch.Te
     return y
 
 
+def matvec_u4_multi(x: torch.Tensor, weights: Sequence[U4Weight],
+                    out_dtypes: Optional[Sequence] = None):
+    """Multi-output fixed FC (iq36_fixed_fc3/4): [W_j x for each W_j] in one launch.
+
+    All matrices share k and group; out_dtypes per output (float16 default).
+    """
+    _require_cuda(x, *[w.qweight for w in weights])
+    count = len(weights)
+    if not 1 <= count <= _lib.AIMA_MAX_MULTI_OUT:
+        raise ValueError(f"1 to {_lib.AIMA_MAX_MULTI_OUT} weight matrices")
+    k, group = weights[0].k, weights[0].group
+    if any(w.k != k or w.group != group for w in weights):
+        raise ValueError("every matrix needs the same k and group")
+    if x.dtype != torch.float16 or x.numel() != k or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float16 vector of length k")
+    dts = list(out_dtypes) if out_dtypes is not None else [torch.float16] * count
+    if len(dts) != count or any(d not in (torch.float16, torch.float32) for d in dts):
+        raise ValueError("one out dtype per matrix, float16 or float32")
+    ys = [torch.empty(w.experts * w.rows, dtype=d, device=x.device) for w, d in zip(weights, dts)]
+    tens = (_lib.U4TensorC * count)(*[_lib.U4TensorC(w.qweight.data_ptr(), w.scale.data_ptr(),
+                                                      w.zp.data_ptr()) for w in weights])
+    ns = (C.c_int64 * count)(*[w.experts * w.rows for w in weights])
+    yp = (C.c_void_p * count)(*[y.data_ptr() for y in ys])
+    od = (C.c_int32 * count)(*[_lib.AIMA_OUT_F32 if d == torch.float32 else _lib.AIMA_OUT_F16
+                               for d in dts])
+    call("aima_u4_matvec_multi", x.data_ptr(), count, tens, ns, k, group, yp, od, _stream())
+    return ys
+
+
+def router_fc_topk(h: torch.Tensor, router: U4Weight, expert_used_count: int = 8,
+                   min_weight_sum: float = MIN_WEIGHT_SUM):
+    """Routing of one token on the device: logits = router · h (U4 FC, f32),
+    then select_router_topk.  Returns (ids int32 [k], weights float32 [k],
+    logits float32 [experts]) (gguf_loader.cpp:5708-5711)."""
+    _require_cuda(h, router.qweight)
+    if h.dtype != torch.float16 or h.numel() != router.k or not h.is_contiguous():
+        raise ValueError("h must be a contiguous float16 vector of length hidden")
+    E = router.experts * router.rows
+    k = int(expert_used_count)
+    if k <= 0 or k > E:
+        raise ValueError("top-k count must be in [1, experts]")
+    logits = torch.empty(E, dtype=torch.float32, device=h.device)
+    ids = torch.empty(k, dtype=torch.int32, device=h.device)
+    w = torch.empty(k, dtype=torch.float32, device=h.device)
+    t = _lib.U4TensorC(router.qweight.data_ptr(), router.scale.data_ptr(), router.zp.data_ptr())
+    call("aima_router_fc_topk", h.data_ptr(), C.byref(t), E, router.k, router.group, k,
+         float(min_weight_sum), logits.data_ptr(), ids.data_ptr(), w.data_ptr(), _stream())
+    return ids, w, logits
+
+
 def apply_rms_norm(x: torch.Tensor, weight: torch.Tensor, epsilon: float) -> torch.Tensor:
     """Row-wise RMSNorm of float16 x [rows, hidden] with float32 weight -> float16."""
     _require_cuda(x, weight)

@@ -417,8 +417,42 @@ def matvec_bench(torch, ops, synth, layers, layers_c, dev, ids_buf, w_buf):
     out["config3_lm_head_N248320"] = {"us": round(us, 2), "gbs": round(b3 / us / 1e3, 1),
                                       "hbm_frac": round(b3 / us / 1e3 / HBM_PEAK_GBS, 4),
                                       "bytes": b3}
+    del wl
+    # the K=2048 fanout (multi-output fixed FC, N = [1, 512, 512, 256]) and the
+    # device router (U4 FC 2048 -> 256, then top-8), each over ~270 MB of
+    # rotating weight copies (past the caches)
+    fan_rows = (1, 512, 512, 256)
+    fan_dts = [torch.float16, torch.float16, torch.float16, torch.float32]
+    fans = [[synth.u4_weight(1, n, 2048, GROUP, gen, dev) for n in fan_rows] for _ in range(200)]
+    xf = synth.activations(1, 2048, 9, dev)[0].contiguous()
+
+    def fan_all():
+        for f in fans:
+            ops.matvec_u4_multi(xf, f, fan_dts)
+
+    rep = graphed(torch, fan_all)
+    us = timed(torch, rep, 5, warmup=1) / len(fans)
+    bf = sum(u4_bytes(n, 2048) for n in fan_rows) + 2048 * 2 + (1 + 512 + 512) * 2 + 256 * 4
+    out["fanout_K2048_N1_512_512_256"] = {"us": round(us, 3), "gbs": round(bf / us / 1e3, 1),
+                                          "hbm_frac": round(bf / us / 1e3 / HBM_PEAK_GBS, 4),
+                                          "bytes": bf}
+    del fans
+    routers = [synth.u4_weight(1, 256, 2048, GROUP, gen, dev) for _ in range(1000)]
+
+    def router_all():
+        for r in routers:
+            ops.router_fc_topk(xf, r, K_TOP)
+
+    rep = graphed(torch, router_all)
+    us = timed(torch, rep, 5, warmup=1) / len(routers)
+    br = u4_bytes(256, 2048) + 2048 * 2 + 256 * 4
+    out["router_fc_topk_E256"] = {"us": round(us, 3), "gbs": round(br / us / 1e3, 1),
+                                  "hbm_frac": round(br / us / 1e3 / HBM_PEAK_GBS, 4), "bytes": br}
+    del routers
     log(f"config0 {out['config0_matvec_K2048_N4096']['us']} us, config1 "
-        f"{out['config1_decode_layer']['us']} us, config3 {out['config3_lm_head_N248320']['us']} us")
+        f"{out['config1_decode_layer']['us']} us, config3 {out['config3_lm_head_N248320']['us']} us, "
+        f"fanout {out['fanout_K2048_N1_512_512_256']['us']} us, router "
+        f"{out['router_fc_topk_E256']['us']} us")
     return out
 
 

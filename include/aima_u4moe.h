@@ -51,6 +51,8 @@ extern "C" {
 
 #define AIMA_OUT_F16 0
 #define AIMA_OUT_F32 1
+/* Most outputs of one aima_u4_matvec_multi call. */
+#define AIMA_MAX_MULTI_OUT 4
 
 /* Device pointers of one U4 matrix or expert stack. */
 typedef struct aima_u4_tensor {
@@ -108,6 +110,20 @@ int aima_u4_matvec(const uint16_t* x, const uint8_t* qweight,
                    int64_t k, int32_t group, void* y, int32_t out_dtype,
                    void* stream);
 
+/* Multi-output U4 matvec over one input: y_j = W_j x for j < count (1 to
+ * AIMA_MAX_MULTI_OUT), W_j = weights[j] with n[j] rows of k, output f16 or f32
+ * per out_dtype[j]; one launch, every block owning rows of one matrix.
+ * Replaces the multi-output fixed FC iq36_fixed_fc3 / iq36_fixed_fc4
+ * (engine/openvino/custom/iq36_fixed_fc_multi_output.cl:9-60: one input,
+ * then weight, out, scale, zp per projection, each workgroup selecting its
+ * projection), which serves the K = 2048 fanout N = [1, 512, 512, 256]
+ * (shared-expert gate scalar, shared gate, shared up, router).  Each y_j is
+ * bit-identical to aima_u4_matvec of W_j; K and group rules as there. */
+int aima_u4_matvec_multi(const uint16_t* x, int32_t count,
+                         const aima_u4_tensor* weights, const int64_t* n,
+                         int64_t k, int32_t group, void* const* y,
+                         const int32_t* out_dtype, void* stream);
+
 /* RMSNorm per row, out = f16(x * (1/sqrt(mean(x^2) + eps)) * weight) with f32
  * arithmetic.  Replaces apply_rms_norm
  * (engine/include/intel_qwen36/gguf_loader.hpp:355-357). */
@@ -123,6 +139,17 @@ int aima_rmsnorm(const uint16_t* x, const float* weight, int64_t rows,
 int aima_router_topk(const float* logits, int64_t tokens, int32_t experts,
                      int32_t k, float min_weight_sum, int32_t* ids,
                      float* weights, void* stream);
+
+/* Router on device for one token: logits = f32 U4 FC of h (router weight
+ * [experts][hidden]), then the selection of aima_router_topk.  Replaces the
+ * reference's routing step router_logits = matvec_tensor(ffn_gate_inp.weight,
+ * ffn_norm); select_router_topk(router_logits, 8, 6.103515625e-5)
+ * (engine/src/gguf_loader.cpp:5708-5711).  logits (experts floats) is a
+ * caller buffer and keeps the logits.  experts <= 1024, k <= 16. */
+int aima_router_fc_topk(const uint16_t* h, const aima_u4_tensor* router,
+                        int32_t experts, int64_t hidden, int32_t group,
+                        int32_t k, float min_weight_sum, float* logits,
+                        int32_t* ids, float* weights, void* stream);
 
 /* Workspace bytes for aima_moe_ffn_decode / aima_moe_stack_decode. */
 int aima_moe_decode_workspace_size(const aima_moe_layer* layer, int32_t k,
