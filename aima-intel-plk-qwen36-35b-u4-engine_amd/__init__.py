@@ -17,6 +17,7 @@ from .ops import (  # noqa: F401
     apply_rms_norm,
     build_grouped_schedule,
     grouped_moe_prefill,
+    lm_head_topk,
     matvec_u4,
     matvec_u4_multi,
     moe_decode_down,
@@ -26,6 +27,7 @@ from .ops import (  # noqa: F401
     router_fc_topk,
     run_moe_ffn_layer,
     select_router_topk,
+    topk_f32,
     u4_dequant,
 )
 from .runtime import (  # noqa: F401

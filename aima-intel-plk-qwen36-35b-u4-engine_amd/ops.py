@@ -169,6 +169,40 @@ def router_fc_topk(h: torch.Tensor, router: U4Weight, expert_used_count: int = 8
     return ids, w, logits
 
 
+def topk_f32(values: torch.Tensor, k: int, ws: Optional[Workspace] = None):
+    """Top-k of a float32 vector on the device: (ids int32 [k], values float32
+    [k]), value descending, lower index first among equal values."""
+    _require_cuda(values)
+    if values.dtype != torch.float32 or values.dim() != 1 or not values.is_contiguous():
+        raise ValueError("values must be a contiguous float32 vector")
+    n = values.numel()
+    ws = _ws(ws, values.device)
+    buf = ws.get(size_query("aima_topk_workspace_size", n, int(k)))
+    ids = torch.empty(int(k), dtype=torch.int32, device=values.device)
+    out = torch.empty(int(k), dtype=torch.float32, device=values.device)
+    call("aima_topk_f32", values.data_ptr(), n, int(k), ids.data_ptr(), out.data_ptr(),
+         buf.data_ptr(), buf.numel(), _stream())
+    return ids, out
+
+
+def lm_head_topk(x: torch.Tensor, w: U4Weight, k: int = 8, ws: Optional[Workspace] = None):
+    """U4 LM head with top-k (q4x8_matvec.cl:973-1021): returns (ids int32 [k],
+    values float32 [k], logits float32 [rows])."""
+    _require_cuda(x, w.qweight)
+    if x.dtype != torch.float16 or x.numel() != w.k or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float16 vector of length k")
+    n = w.experts * w.rows
+    ws = _ws(ws, x.device)
+    buf = ws.get(size_query("aima_topk_workspace_size", n, int(k)))
+    logits = torch.empty(n, dtype=torch.float32, device=x.device)
+    ids = torch.empty(int(k), dtype=torch.int32, device=x.device)
+    vals = torch.empty(int(k), dtype=torch.float32, device=x.device)
+    call("aima_u4_lm_head_topk", x.data_ptr(), w.qweight.data_ptr(), w.scale.data_ptr(),
+         w.zp.data_ptr(), n, w.k, w.group, int(k), logits.data_ptr(), ids.data_ptr(),
+         vals.data_ptr(), buf.data_ptr(), buf.numel(), _stream())
+    return ids, vals, logits
+
+
 def apply_rms_norm(x: torch.Tensor, weight: torch.Tensor, epsilon: float) -> torch.Tensor:
     """Row-wise RMSNorm of float16 x [rows, hidden] with float32 weight -> float16."""
     _require_cuda(x, weight)

@@ -417,6 +417,12 @@ def matvec_bench(torch, ops, synth, layers, layers_c, dev, ids_buf, w_buf):
     out["config3_lm_head_N248320"] = {"us": round(us, 2), "gbs": round(b3 / us / 1e3, 1),
                                       "hbm_frac": round(b3 / us / 1e3 / HBM_PEAK_GBS, 4),
                                       "bytes": b3}
+    # the same LM head with its top-8 (logits kept, two selection passes)
+    lws = ops.Workspace(dev)
+    us = timed(torch, lambda: ops.lm_head_topk(xl, wl, 8, ws=lws), 50, warmup=5)
+    out["lm_head_topk8_N248320"] = {"us": round(us, 2), "gbs": round(b3 / us / 1e3, 1),
+                                    "hbm_frac": round(b3 / us / 1e3 / HBM_PEAK_GBS, 4),
+                                    "bytes": b3}
     del wl
     # the K=2048 fanout (multi-output fixed FC, N = [1, 512, 512, 256]) and the
     # device router (U4 FC 2048 -> 256, then top-8), each over ~270 MB of

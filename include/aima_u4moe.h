@@ -151,6 +151,28 @@ int aima_router_fc_topk(const uint16_t* h, const aima_u4_tensor* router,
                         int32_t k, float min_weight_sum, float* logits,
                         int32_t* ids, float* weights, void* stream);
 
+/* Workspace bytes for aima_topk_f32 / aima_u4_lm_head_topk over n values. */
+int aima_topk_workspace_size(int64_t n, int32_t k, size_t* bytes);
+
+/* Top-k of n f32 values (an LM head's logits): ids[r], values[r] for ranks
+ * r < k, value descending, the lower index first among equal values (the
+ * order of the reference's LM-head partial top-8, q4x8_matvec.cl:973-1021).
+ * n <= 1,048,576, k <= 16; the workspace may be null when n <= 1024. */
+int aima_topk_f32(const float* values, int64_t n, int32_t k, int32_t* ids,
+                  float* out_values, void* workspace, size_t workspace_bytes,
+                  void* stream);
+
+/* U4 LM head with top-k: logits = f32 U4 matvec of x (as aima_u4_matvec,
+ * kept in the caller's logits buffer of n floats), then aima_topk_f32 over
+ * them.  Replaces the reference's q4s_group128_lm_head_topk8_f32
+ * (engine/gpu/opencl/q4x8_matvec.cl:973-1021: logits out plus per-block
+ * partial top-8 ids and values) with its merge. */
+int aima_u4_lm_head_topk(const uint16_t* x, const uint8_t* qweight,
+                         const uint16_t* scale, const uint8_t* zp, int64_t n,
+                         int64_t k, int32_t group, int32_t topk, float* logits,
+                         int32_t* ids, float* values, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* Workspace bytes for aima_moe_ffn_decode / aima_moe_stack_decode. */
 int aima_moe_decode_workspace_size(const aima_moe_layer* layer, int32_t k,
                                    size_t* bytes);

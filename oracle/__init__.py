@@ -246,6 +246,27 @@ def top_k_indices(values, k: int) -> np.ndarray:
     return out
 
 
+def lm_head_topk(values, k: int = 8, block: int = 256):
+    """Top-k of an LM head's logits as the reference builds it
+    (engine/gpu/opencl/q4x8_matvec.cl:973-1021): every block of 256 rows
+    keeps its best k by insertion -- a candidate moves past every kept value
+    >= itself, so an earlier index stays ahead of an equal later value -- and
+    the per-block lists merge under the same order.  A stable sort on the
+    negated values reproduces each insertion.  Returns (ids int32 [k],
+    values f32 [k]); NaNs sort last."""
+    v = _f32(values).reshape(-1)
+    cand_v, cand_i = [], []
+    for b0 in range(0, v.size, block):
+        seg = v[b0:b0 + block]
+        order = np.argsort(-seg, kind="stable")[:k]
+        cand_v.append(seg[order])
+        cand_i.append(order.astype(np.int64) + b0)
+    cv = np.concatenate(cand_v)
+    ci = np.concatenate(cand_i)
+    top = np.argsort(-cv, kind="stable")[:k]
+    return ci[top].astype(np.int32), cv[top].astype(np.float32)
+
+
 def normalize_weights(w, min_weight_sum: float) -> np.ndarray:
     w = _f32(w).reshape(-1)
     out = np.empty_like(w)
