@@ -24,11 +24,14 @@ from .ops import (  # noqa: F401
     moe_decode_gate_up,
     moe_stack_decode,
     moe_stack_prefill,
+    q4k_unpack,
     router_fc_topk,
     run_moe_ffn_layer,
     select_router_topk,
     topk_f32,
     u4_dequant,
+    u4_group_major_to_rows,
+    u4_rows_to_group_major,
 )
 from .runtime import (  # noqa: F401
     GroupedU4PrefillInput,

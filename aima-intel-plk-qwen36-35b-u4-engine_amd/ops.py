@@ -169,6 +169,52 @@ def router_fc_topk(h: torch.Tensor, router: U4Weight, expert_used_count: int = 8
     return ids, w, logits
 
 
+def u4_group_major_to_rows(scale_gm: torch.Tensor, zp_gm: torch.Tensor, n: int, groups: int):
+    """Group-major scale f16 [groups][n] and zero points (packed over the
+    group-major flat index) -> the boundary row-major order."""
+    _require_cuda(scale_gm, zp_gm)
+    if scale_gm.dtype != torch.float16 or zp_gm.dtype != torch.uint8:
+        raise TypeError("scale must be float16 and zero points uint8")
+    if scale_gm.numel() != n * groups or zp_gm.numel() != (n * groups + 1) // 2:
+        raise ValueError("scale / zero-point sizes do not match n * groups")
+    scale = torch.empty(n * groups, dtype=torch.float16, device=scale_gm.device)
+    zp = torch.empty((n * groups + 1) // 2, dtype=torch.uint8, device=scale_gm.device)
+    call("aima_u4_group_major_to_rows", scale_gm.contiguous().data_ptr(),
+         zp_gm.contiguous().data_ptr(), n, groups, scale.data_ptr(), zp.data_ptr(), _stream())
+    return scale.reshape(n, groups), zp
+
+
+def u4_rows_to_group_major(scale: torch.Tensor, zp: torch.Tensor, n: int, groups: int):
+    """Boundary row-major scale / zero points -> the group-major package order
+    (tools/intel_qwen36_openvino_fixed_fc.py:218-265)."""
+    _require_cuda(scale, zp)
+    if scale.dtype != torch.float16 or zp.dtype != torch.uint8:
+        raise TypeError("scale must be float16 and zero points uint8")
+    if scale.numel() != n * groups or zp.numel() != (n * groups + 1) // 2:
+        raise ValueError("scale / zero-point sizes do not match n * groups")
+    scale_gm = torch.empty(n * groups, dtype=torch.float16, device=scale.device)
+    zp_gm = torch.empty((n * groups + 1) // 2, dtype=torch.uint8, device=scale.device)
+    call("aima_u4_rows_to_group_major", scale.contiguous().data_ptr(), zp.contiguous().data_ptr(),
+         n, groups, scale_gm.data_ptr(), zp_gm.data_ptr(), _stream())
+    return scale_gm.reshape(groups, n), zp_gm
+
+
+def q4k_unpack(blocks: torch.Tensor, rows: int, cols: int):
+    """GGUF Q4_K [rows][cols] (144-byte super-blocks) -> (codes uint8
+    [rows][cols/2] in the boundary packing, scale float16 [rows][cols/32],
+    min float32 [rows][cols/32]); value = scale * q - min."""
+    _require_cuda(blocks)
+    if blocks.dtype != torch.uint8 or cols % 256 or blocks.numel() != rows * (cols // 256) * 144:
+        raise ValueError("blocks must be uint8 [rows][cols/256][144]")
+    dev = blocks.device
+    q = torch.empty((rows, cols // 2), dtype=torch.uint8, device=dev)
+    sc = torch.empty((rows, cols // 32), dtype=torch.float16, device=dev)
+    mn = torch.empty((rows, cols // 32), dtype=torch.float32, device=dev)
+    call("aima_q4k_unpack", blocks.contiguous().data_ptr(), rows, cols, q.data_ptr(), sc.data_ptr(),
+         mn.data_ptr(), _stream())
+    return q, sc, mn
+
+
 def topk_f32(values: torch.Tensor, k: int, ws: Optional[Workspace] = None):
     """Top-k of a float32 vector on the device: (ids int32 [k], values float32
     [k]), value descending, lower index first among equal values."""

@@ -151,6 +151,33 @@ int aima_router_fc_topk(const uint16_t* h, const aima_u4_tensor* router,
                         int32_t k, float min_weight_sum, float* logits,
                         int32_t* ids, float* weights, void* stream);
 
+/* Scale / zero-point order conversions for an [n][groups] U4 matrix: the
+ * boundary order is row-major (scale f16[n][groups], zero points over the
+ * flat n*groups index, low nibble first), which is also the order of an
+ * OpenVINO IR U4 FC (tools/intel_qwen36_openvino_fixed_fc.py:107-144); the
+ * reference's fixed-FC package stores both group-major, [groups][n]
+ * (tools/intel_qwen36_openvino_fixed_fc.py:218-265, same nibble packing).
+ * n * groups must be even (as the reference requires).  qweight is the same
+ * in both orders. */
+int aima_u4_group_major_to_rows(const uint16_t* scale_gm, const uint8_t* zp_gm,
+                                int64_t n, int64_t groups, uint16_t* scale,
+                                uint8_t* zp, void* stream);
+int aima_u4_rows_to_group_major(const uint16_t* scale, const uint8_t* zp,
+                                int64_t n, int64_t groups, uint16_t* scale_gm,
+                                uint8_t* zp_gm, void* stream);
+
+/* GGUF Q4_K unpack of a [rows][cols] tensor (144-byte super-blocks of 256
+ * values): codes in the boundary packing (qweight u8[rows][cols/2]), the
+ * group-32 scale f16(d * sc) (f16[rows][cols/32]) and min dmin * m
+ * (f32[rows][cols/32]); the value is scale * q - min.  The package the
+ * reference's prepack builds from Q4_K
+ * (tools/intel-qwen36-openvino-moe-micro-prepack.py:76-124), row-major.
+ * cols % 256 == 0.  (The boundary matvec takes integer zero points, not
+ * mins: Q4_K weights reach it only through a requantization, not done here.) */
+int aima_q4k_unpack(const uint8_t* blocks, int64_t rows, int64_t cols,
+                    uint8_t* qweight, uint16_t* scale, float* mins,
+                    void* stream);
+
 /* Workspace bytes for aima_topk_f32 / aima_u4_lm_head_topk over n values. */
 int aima_topk_workspace_size(int64_t n, int32_t k, size_t* bytes);
 

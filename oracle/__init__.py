@@ -267,6 +267,84 @@ def lm_head_topk(values, k: int = 8, block: int = 256):
     return ci[top].astype(np.int32), cv[top].astype(np.float32)
 
 
+def u4_nibbles(packed, count: int) -> np.ndarray:
+    """Packed u4 stream (low nibble = even index) -> count codes."""
+    p = np.asarray(packed, np.uint8).reshape(-1)
+    out = np.empty(p.size * 2, np.uint8)
+    out[0::2] = p & 0x0F
+    out[1::2] = p >> 4
+    return out[:count]
+
+
+def u4_pack(codes) -> np.ndarray:
+    c = np.asarray(codes, np.uint8).reshape(-1)
+    if c.size % 2:
+        c = np.concatenate([c, np.zeros(1, np.uint8)])
+    return (c[0::2] & 0x0F) | ((c[1::2] & 0x0F) << 4)
+
+
+def group_major_scale(scale, n: int, groups: int) -> np.ndarray:
+    """f16 scale [n][groups] -> [groups][n]
+    (tools/intel_qwen36_openvino_fixed_fc.py:218-229)."""
+    return np.ascontiguousarray(np.asarray(scale, np.uint16).reshape(n, groups).T)
+
+
+def group_major_zero_point(zp, n: int, groups: int) -> np.ndarray:
+    """u4 zero points over [n][groups] -> packed over [groups][n]
+    (tools/intel_qwen36_openvino_fixed_fc.py:241-265)."""
+    logical = u4_nibbles(zp, n * groups).reshape(n, groups)
+    return u4_pack(np.ascontiguousarray(logical.T))
+
+
+def rows_from_group_major(scale_gm, zp_gm, n: int, groups: int):
+    """Inverse of group_major_scale / group_major_zero_point."""
+    scale = np.ascontiguousarray(np.asarray(scale_gm, np.uint16).reshape(groups, n).T)
+    zp = u4_pack(np.ascontiguousarray(u4_nibbles(zp_gm, n * groups).reshape(groups, n).T))
+    return scale, zp
+
+
+Q4K_VALUES = 256
+Q4K_BYTES = 144
+
+
+def q4k_scale_min(packed12, j: int):
+    """6-bit scale and min of sub-block j from the 12 packed bytes of a Q4_K
+    super-block (tools/intel-qwen36-openvino-moe-micro-prepack.py:76-88)."""
+    q = [int(v) for v in packed12]
+    if j < 4:
+        return q[j] & 63, q[j + 4] & 63
+    return (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4), (q[j + 4] >> 4) | ((q[j] >> 6) << 4)
+
+
+def q4k_unpack(raw, rows: int, cols: int):
+    """Q4_K [rows][cols] -> (codes u8 [rows][cols/2] boundary packing, scale
+    f16 bits [rows][cols/32] = f16(d * sc), min f32 [rows][cols/32] = dmin * m)
+    (tools/intel-qwen36-openvino-moe-micro-prepack.py:91-124; row-major)."""
+    bpr = cols // Q4K_VALUES
+    b = np.asarray(raw, np.uint8).reshape(rows, bpr, Q4K_BYTES)
+    codes = np.empty((rows, cols), np.uint8)
+    qs = b[:, :, 16:]
+    for s in range(4):
+        seg = qs[:, :, 32 * s:32 * s + 32]
+        for blk in range(bpr):
+            base = blk * Q4K_VALUES + 64 * s
+            codes[:, base:base + 32] = seg[:, blk] & 0x0F
+            codes[:, base + 32:base + 64] = seg[:, blk] >> 4
+    d = b[:, :, 0:2].copy().view("<f2").reshape(rows, bpr).astype(np.float32)
+    dmin = b[:, :, 2:4].copy().view("<f2").reshape(rows, bpr).astype(np.float32)
+    sc = np.empty((rows, bpr, 8), np.float32)
+    mn = np.empty((rows, bpr, 8), np.float32)
+    for r in range(rows):
+        for blk in range(bpr):
+            for j in range(8):
+                s6, m6 = q4k_scale_min(b[r, blk, 4:16], j)
+                sc[r, blk, j] = np.float32(d[r, blk]) * np.float32(s6)
+                mn[r, blk, j] = np.float32(dmin[r, blk]) * np.float32(m6)
+    packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
+    scale = sc.reshape(rows, bpr * 8).astype(np.float16).view(np.uint16)
+    return packed, scale, mn.reshape(rows, bpr * 8)
+
+
 def normalize_weights(w, min_weight_sum: float) -> np.ndarray:
     w = _f32(w).reshape(-1)
     out = np.empty_like(w)
