@@ -23,6 +23,7 @@ from .ops import (  # noqa: F401
     moe_decode_down,
     moe_decode_gate_up,
     moe_stack_decode,
+    moe_stack_decode_routed,
     moe_stack_prefill,
     q4k_unpack,
     router_fc_topk,

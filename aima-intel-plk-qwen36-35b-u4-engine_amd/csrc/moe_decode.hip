@@ -24,19 +24,22 @@ constexpr int kDownRowsPerBlock = 8;
 constexpr int kDownThreads = 512;      // 8 waves, wave w owns slots w, w + 8, w + 16
 constexpr int kDownSlotsPerWave = 3;   // slots per wave per batch of 24
 
+constexpr int kStackMaxExperts = 1024;  // router logits room in the stack workspace
+
 struct DecodeWs {
   uint32_t* err;
   uint16_t* act;   // [(k+1)][I] f16
   float* sigma;    // shared-expert gate
   uint16_t* h;     // [H] normalized input (stack only)
   uint16_t* r[2];  // [H] residual ping-pong (stack only)
+  float* logits;   // [<= 1024] router logits (stack only)
 };
 
 static size_t decode_ws_bytes(int64_t hidden, int64_t inter, int k, bool stack) {
   size_t b = kWsHeader;
   b += round_up((size_t)(k + 1) * inter * 2, 256);
   b += 256;
-  if (stack) b += 3 * round_up((size_t)hidden * 2, 256);
+  if (stack) b += 3 * round_up((size_t)hidden * 2, 256) + kStackMaxExperts * 4;
   return b;
 }
 
@@ -55,6 +58,8 @@ static DecodeWs decode_ws(void* ws, int64_t hidden, int64_t inter, int k, bool s
     w.r[0] = reinterpret_cast<uint16_t*>(p);
     p += round_up((size_t)hidden * 2, 256);
     w.r[1] = reinterpret_cast<uint16_t*>(p);
+    p += round_up((size_t)hidden * 2, 256);
+    w.logits = reinterpret_cast<float*>(p);
   }
   return w;
 }
@@ -403,6 +408,12 @@ static int decode_layer(const aima_moe_layer& L, const uint16_t* x, const uint16
 
 int rmsnorm_launch(const uint16_t* x, const float* weight, int64_t rows, int64_t hidden,
                    float eps, uint16_t* out, hipStream_t st);
+int u4_matvec_dispatch(const uint16_t* x, const uint8_t* qw, const uint16_t* scale,
+                       const uint8_t* zp, int64_t n, int64_t k, int glog2, void* y,
+                       int out_f32, hipStream_t st);
+int router_topk_launch(const float* logits, int64_t tokens, int experts, int k,
+                       float min_weight_sum, int32_t* ids, float* weights, hipStream_t st);
+int group_log2_of(int group);
 
 }  // namespace aima
 
@@ -516,6 +527,59 @@ extern "C" int aima_moe_stack_decode(const aima_moe_layer* layers, int32_t n_lay
     if (rc != AIMA_OK) return rc;
     uint16_t* dst = (l == n_layers - 1) ? out : w.r[l & 1];
     rc = decode_layer(L, w.h, r, ids + (int64_t)l * k, weights + (int64_t)l * k, k, dst, w, st);
+    if (rc != AIMA_OK) return rc;
+    r = dst;
+  }
+  return AIMA_OK;
+}
+
+extern "C" int aima_moe_stack_decode_routed(const aima_moe_layer* layers,
+                                            const aima_u4_tensor* routers, int32_t n_layers,
+                                            float eps, const uint16_t* residual_in, int32_t k,
+                                            float min_weight_sum, int32_t* ids, float* weights,
+                                            uint16_t* out, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  AIMA_REQUIRE(layers && routers && n_layers > 0, "moe_stack_decode_routed: need layers");
+  AIMA_REQUIRE(residual_in && ids && weights && out, "moe_stack_decode_routed: null pointer");
+  AIMA_REQUIRE(min_weight_sum > 0.f, "moe_stack_decode_routed: minimum weight sum must be positive");
+  for (int32_t l = 0; l < n_layers; ++l) {
+    int rc = check_layer(&layers[l], k, true);
+    if (rc != AIMA_OK) return rc;
+    AIMA_REQUIRE(layers[l].hidden == layers[0].hidden && layers[l].inter == layers[0].inter,
+                 "moe_stack_decode_routed: all layers must share hidden and inter");
+    AIMA_REQUIRE(routers[l].qweight && routers[l].scale && routers[l].zp,
+                 "moe_stack_decode_routed: null router tensor");
+    AIMA_REQUIRE(aligned(routers[l].qweight, 16), "moe_stack_decode_routed: router qweight alignment");
+    AIMA_REQUIRE(layers[l].experts <= kStackMaxExperts && k <= 16,
+                 "moe_stack_decode_routed: experts <= 1024 and k <= 16");
+    AIMA_REQUIRE(group_log2_of(layers[l].group) > 0,
+                 "moe_stack_decode_routed: group must be 32, 64, 128 or 256");
+  }
+  if (!decode_shape_ok(&layers[0])) {
+    return fail(AIMA_E_UNSUPPORTED, "moe_stack_decode_routed: unsupported hidden/inter");
+  }
+  const size_t need = decode_ws_bytes(layers[0].hidden, layers[0].inter, k, true);
+  if (!workspace || workspace_bytes < need) {
+    return fail(AIMA_E_WORKSPACE, "moe_stack_decode_routed: workspace missing or too small");
+  }
+  AIMA_REQUIRE(aligned(workspace, 256), "moe_stack_decode_routed: workspace must be 256-byte aligned");
+  const DecodeWs w = decode_ws(workspace, layers[0].hidden, layers[0].inter, k, true);
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* r = residual_in;
+  for (int32_t l = 0; l < n_layers; ++l) {
+    const aima_moe_layer& L = layers[l];
+    int rc = rmsnorm_launch(r, L.norm_weight, 1, L.hidden, eps, w.h, st);
+    if (rc != AIMA_OK) return rc;
+    // routing from this layer's normalized input (gguf_loader.cpp:5708-5711)
+    rc = u4_matvec_dispatch(w.h, routers[l].qweight, routers[l].scale, routers[l].zp, L.experts,
+                            L.hidden, group_log2_of(L.group), w.logits, 1, st);
+    if (rc != AIMA_OK) return rc;
+    int32_t* ids_l = ids + (int64_t)l * k;
+    float* w_l = weights + (int64_t)l * k;
+    rc = router_topk_launch(w.logits, 1, L.experts, k, min_weight_sum, ids_l, w_l, st);
+    if (rc != AIMA_OK) return rc;
+    uint16_t* dst = (l == n_layers - 1) ? out : w.r[l & 1];
+    rc = decode_layer(L, w.h, r, ids_l, w_l, k, dst, w, st);
     if (rc != AIMA_OK) return rc;
     r = dst;
   }

@@ -319,6 +319,12 @@ static void launch_router_topk(const float* logits, int64_t tokens, int experts,
   }
 }
 
+int router_topk_launch(const float* logits, int64_t tokens, int experts, int k,
+                       float min_weight_sum, int32_t* ids, float* weights, hipStream_t st) {
+  launch_router_topk(logits, tokens, experts, k, min_weight_sum, ids, weights, st);
+  return launch_check("router_topk");
+}
+
 int u4_matvec_dispatch(const uint16_t* x, const uint8_t* qw, const uint16_t* scale,
                        const uint8_t* zp, int64_t n, int64_t k, int glog2, void* y,
                        int out_f32, hipStream_t st) {

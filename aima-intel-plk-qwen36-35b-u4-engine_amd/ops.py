@@ -427,6 +427,38 @@ def moe_stack_decode(layers: Sequence[MoeLayerWeights], residual: torch.Tensor,
     return out
 
 
+def moe_stack_decode_routed(layers: Sequence[MoeLayerWeights], routers: Sequence[U4Weight],
+                            residual: torch.Tensor, expert_used_count: int = 8,
+                            epsilon: float = 1e-6, min_weight_sum: float = MIN_WEIGHT_SUM,
+                            ws: Optional[Workspace] = None):
+    """True decode of one token: every layer routes from its own normalized
+    input (router U4 FC [experts][hidden], then select_router_topk).
+    Returns (out f16 [H], ids int32 [L, k], weights float32 [L, k])."""
+    _require_cuda(residual, *[r.qweight for r in routers])
+    L = len(layers)
+    if len(routers) != L:
+        raise ValueError("one router per layer")
+    H = layers[0].hidden
+    if residual.dtype != torch.float16 or residual.numel() != H:
+        raise ValueError("residual must be float16 [hidden]")
+    for lay, r in zip(layers, routers):
+        if r.experts * r.rows != lay.experts or r.k != H or r.group != lay.group:
+            raise ValueError("router must be [experts][hidden] at the layer's group")
+    k = int(expert_used_count)
+    arr = _layers_c(layers)
+    rt = (_lib.U4TensorC * L)(*[_lib.U4TensorC(r.qweight.data_ptr(), r.scale.data_ptr(),
+                                                r.zp.data_ptr()) for r in routers])
+    ws = _ws(ws, residual.device)
+    buf = ws.get(size_query("aima_moe_decode_workspace_size", C.byref(arr[0]), k))
+    out = torch.empty(H, dtype=torch.float16, device=residual.device)
+    ids = torch.empty((L, k), dtype=torch.int32, device=residual.device)
+    w = torch.empty((L, k), dtype=torch.float32, device=residual.device)
+    call("aima_moe_stack_decode_routed", arr, rt, L, float(epsilon), residual.data_ptr(), k,
+         float(min_weight_sum), ids.data_ptr(), w.data_ptr(), out.data_ptr(), buf.data_ptr(),
+         buf.numel(), _stream())
+    return out, ids, w
+
+
 def moe_stack_prefill(layers: Sequence[MoeLayerWeights], x: torch.Tensor, ids: torch.Tensor,
                       weights: torch.Tensor, epsilon: float = 1e-6,
                       ws: Optional[Workspace] = None, out: Optional[torch.Tensor] = None,

@@ -243,6 +243,16 @@ def main():
     multi_us = timed(torch, decode_step_multikernel, max(10, args.steps // 10), warmup=3)
     log(f"decode multi-kernel: {multi_us:.1f} us/token")
     ws.check()
+    # true decode: each layer routes from its own hidden state (router U4 FC
+    # [256][2048] + top-8 per layer, then the layer), multi-kernel
+    routers = [synth.u4_weight(1, E, H, GROUP, synth.generator(2041 + l, dev), dev)
+               for l in range(LAYERS)]
+    routed_us = timed(torch, lambda: ops.moe_stack_decode_routed(layers, routers, x, K_TOP,
+                                                                 epsilon=EPS, ws=ws),
+                      max(10, args.steps // 10), warmup=3)
+    log(f"decode multi-kernel, routed from h: {routed_us:.1f} us/token")
+    ws.check()
+    del routers
     plan = ops.DecodePlan(layers, k=K_TOP)
 
     def decode_step():
@@ -288,6 +298,7 @@ def main():
         "decode": {"us_per_token": round(step_us, 2), "eager_us": round(eager_us, 2),
                    "graph_us": round(graph_us, 2), "mode": decode_mode,
                    "multikernel_us": round(multi_us, 2),
+                   "routed_multikernel_us": round(routed_us, 2),
                    "algorithmic_bytes": weight_bytes + act_bytes,
                    "hbm_gbs": round(decode_gbs, 1),
                    "hbm_frac": round(decode_gbs / HBM_PEAK_GBS, 4),

@@ -295,6 +295,20 @@ int aima_moe_stack_decode(const aima_moe_layer* layers, int32_t n_layers,
                           uint16_t* out, void* workspace,
                           size_t workspace_bytes, void* stream);
 
+/* True decode: aima_moe_stack_decode with each layer's routing computed on
+ * the device from its own normalized input -- logits = U4 FC (routers[l],
+ * [experts][hidden], the layer's group) of h_l, then the selection of
+ * aima_router_topk -- as run_qwen36_moe_ffn_layer does per layer
+ * (engine/src/gguf_loader.cpp:5704-5711).  The chosen ids / weights of every
+ * layer are written to ids / weights ([n_layers][k]).  experts <= 1024,
+ * k <= 16; workspace as aima_moe_stack_decode. */
+int aima_moe_stack_decode_routed(const aima_moe_layer* layers,
+                                 const aima_u4_tensor* routers, int32_t n_layers,
+                                 float eps, const uint16_t* residual_in, int32_t k,
+                                 float min_weight_sum, int32_t* ids, float* weights,
+                                 uint16_t* out, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* Resident decode plan: the whole n_layers-layer decode step in ONE
  * persistent launch (hidden 2048, inter 512, k <= 8; see
  * moe_decode_persistent.hip).  create() validates the shapes, checks that
