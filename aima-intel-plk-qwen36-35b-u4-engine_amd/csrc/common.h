@@ -120,6 +120,42 @@ __device__ __forceinline__ float segment_sum(float v) {
   return v;
 }
 
+// Wave-wide best (value, index) pair: larger value, then smaller index.
+// DPP steps inside each 16-lane row, then the four row winners read out and
+// combined in a fixed order; the result is wave-uniform.  Every lane of the
+// wave must be active.
+__device__ __forceinline__ bool pair_better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+template <int CTRL>
+__device__ __forceinline__ void pair_step(float& bv, int& bi) {
+  const float ov = dpp_mov<CTRL>(bv);
+  const int oi = __builtin_amdgcn_update_dpp(0, bi, CTRL, 0xF, 0xF, false);
+  if (pair_better(ov, oi, bv, bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+__device__ __forceinline__ void wave_best_pair(float& bv, int& bi) {
+  pair_step<0xB1>(bv, bi);   // quad_perm [1,0,3,2]
+  pair_step<0x4E>(bv, bi);   // quad_perm [2,3,0,1]
+  pair_step<0x141>(bv, bi);  // row_half_mirror
+  pair_step<0x140>(bv, bi);  // row_mirror
+  float cv = lane_read(bv, 0);
+  int ci = __builtin_amdgcn_readlane(bi, 0);
+#pragma unroll
+  for (int row = 1; row < 4; ++row) {
+    const float ov = lane_read(bv, 16 * row);
+    const int oi = __builtin_amdgcn_readlane(bi, 16 * row);
+    if (pair_better(ov, oi, cv, ci)) {
+      cv = ov;
+      ci = oi;
+    }
+  }
+  bv = cv;
+  bi = ci;
+}
+
 // ---------------------------------------------------------------------------
 // U4 x f16 chunk dot product (32 nibbles of one row against 32 activations).
 //

@@ -7,10 +7,10 @@
 // ahead of a number.
 //
 // Two passes.  Pass 1: P blocks of 1024 threads, block b owns a contiguous
-// chunk of at most 4096 values (4 per thread); each wave picks its k best by
-// k rounds of a wave-wide (value, index) maximum, the 16 wave lists meet in
-// LDS and wave 0 picks the block's k best from them.  Pass 2: one block runs
-// the same selection over the P * k (value, index) candidates.  P <= 256, so
+// chunk of at most 4096 values (4 per thread) and picks its k best (a
+// threshold filter, then k rounds of a wave-wide (value, index) maximum over
+// the survivors; see topk_pass_kernel).  Pass 2: one block runs the same
+// selection over the P * k (value, index) candidates.  P <= 256, so
 // n <= 1,048,576 and the candidates of pass 2 fit one block.
 #include "common.h"
 
@@ -55,15 +55,7 @@ __device__ __forceinline__ void wave_topk(float (&v)[PER], int (&ix)[PER], int k
         bi = ix[j];
       }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (better(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
-    }
+    wave_best_pair(bv, bi);
     if (lane == r) {
       out_v = bv;
       out_i = bi;
@@ -79,12 +71,28 @@ __device__ __forceinline__ void wave_topk(float (&v)[PER], int (&ix)[PER], int k
   }
 }
 
+constexpr int kWaves = kPassThreads / 64;
+constexpr int kMaxCand = 256;  // candidates one wave selects from (4 per lane)
+
 // idx null: a value's index is its position.
+//
+// Threshold filter first: each wave finds its best (value, index) pair; the
+// k-th best of the 16 wave bests, T, bounds the block's top-k from below
+// (the k wave bests at or above T are k pairs at least as good), so only
+// pairs at or above T can be picked.  They are compacted into LDS (ballots
+// give each its slot) and wave 0 selects from them.  When ties leave more
+// than kMaxCand such pairs, every wave selects its own k and wave 0 merges
+// the 16 lists instead.
 __global__ __launch_bounds__(kPassThreads) void topk_pass_kernel(
     const float* __restrict__ vals, const int32_t* __restrict__ idx, int64_t n, int64_t chunk,
     int k, float* __restrict__ out_v, int32_t* __restrict__ out_i) {
-  __shared__ float s_v[(kPassThreads / 64) * kTopkMax];
-  __shared__ int s_i[(kPassThreads / 64) * kTopkMax];
+  __shared__ float s_v[kWaves * kTopkMax];
+  __shared__ int s_i[kWaves * kTopkMax];
+  __shared__ float s_wv[kWaves];
+  __shared__ int s_wi[kWaves];
+  __shared__ int s_cnt[kWaves];
+  __shared__ float s_cv[kMaxCand];
+  __shared__ int s_ci[kMaxCand];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t base = (int64_t)blockIdx.x * chunk;
@@ -102,6 +110,100 @@ __global__ __launch_bounds__(kPassThreads) void topk_pass_kernel(
       ix[j] = kNoIndex;
     }
   }
+  // wave bests
+  float bv = -INFINITY;
+  int bi = kNoIndex;
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    if (better(v[j], ix[j], bv, bi)) {
+      bv = v[j];
+      bi = ix[j];
+    }
+  }
+  wave_best_pair(bv, bi);
+  if (lane == 0) {
+    s_wv[wave] = bv;
+    s_wi[wave] = bi;
+  }
+  __syncthreads();
+  // T = the k-th best wave best: lane w < 16 ranks wave best w against all 16
+  float tv = -INFINITY;
+  int ti = kNoIndex;
+  {
+    int rank = kWaves;
+    float mv = -INFINITY;
+    int mi = kNoIndex;
+    if (lane < kWaves) {
+      mv = s_wv[lane];
+      mi = s_wi[lane];
+      rank = 0;
+      for (int w = 0; w < kWaves; ++w) rank += better(s_wv[w], s_wi[w], mv, mi) ? 1 : 0;
+    }
+    // no rank k-1 (fewer than k waves hold values, their empty bests tie):
+    // no filter, every valid pair qualifies
+    const uint64_t hit = __ballot(rank == k - 1);
+    if (hit) {
+      const int src = (int)__builtin_ctzll(hit);
+      tv = lane_read(mv, src);
+      ti = __builtin_amdgcn_readlane(mi, src);
+    }
+  }
+  // compact the pairs at or above T
+  int cnt = 0;
+  bool q[kPerThread];
+  uint64_t mask[kPerThread];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    q[j] = ix[j] != kNoIndex && (better(v[j], ix[j], tv, ti) || (v[j] == tv && ix[j] == ti));
+    mask[j] = __ballot(q[j]);
+    cnt += __builtin_popcountll(mask[j]);
+  }
+  if (lane == 0) s_cnt[wave] = cnt;
+  __syncthreads();
+  int wbase = 0, total = 0;
+  for (int w = 0; w < kWaves; ++w) {
+    const int c = s_cnt[w];
+    wbase += w < wave ? c : 0;
+    total += c;
+  }
+  if (total <= kMaxCand) {
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int off = wbase;
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+      if (q[j]) {
+        const int slot = off + __builtin_popcountll(mask[j] & below);
+        s_cv[slot] = v[j];
+        s_ci[slot] = ix[j];
+      }
+      off += __builtin_popcountll(mask[j]);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      float c[kMaxCand / 64];
+      int ci[kMaxCand / 64];
+#pragma unroll
+      for (int j = 0; j < kMaxCand / 64; ++j) {
+        const int slot = lane + 64 * j;
+        if (slot < total) {
+          c[j] = s_cv[slot];
+          ci[j] = s_ci[slot];
+        } else {
+          c[j] = -INFINITY;
+          ci[j] = kNoIndex;
+        }
+      }
+      float wv;
+      int wi;
+      wave_topk<kMaxCand / 64>(c, ci, k, wv, wi);
+      if (lane < k) {
+        out_v[(int64_t)blockIdx.x * k + lane] = wv;
+        out_i[(int64_t)blockIdx.x * k + lane] = wi;
+      }
+    }
+    return;
+  }
+  // many ties at the threshold: per-wave selection, then a merge
   float wv;
   int wi;
   wave_topk<kPerThread>(v, ix, k, wv, wi);
@@ -111,15 +213,15 @@ __global__ __launch_bounds__(kPassThreads) void topk_pass_kernel(
   }
   __syncthreads();
   if (wave == 0) {
-    constexpr int kCandPer = (kPassThreads / 64) * kTopkMax / 64;
+    constexpr int kCandPer = kWaves * kTopkMax / 64;
     float c[kCandPer];
     int ci[kCandPer];
 #pragma unroll
     for (int j = 0; j < kCandPer; ++j) {
-      const int q = lane + 64 * j;
-      if (q < (kPassThreads / 64) * k) {
-        c[j] = s_v[q];
-        ci[j] = s_i[q];
+      const int qi = lane + 64 * j;
+      if (qi < kWaves * k) {
+        c[j] = s_v[qi];
+        ci[j] = s_i[qi];
       } else {
         c[j] = -INFINITY;
         ci[j] = kNoIndex;

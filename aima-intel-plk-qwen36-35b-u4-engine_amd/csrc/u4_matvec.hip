@@ -269,15 +269,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
         bi = i;
       }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      const float op = __shfl_xor(bp, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (op > bp || (op == bp && oi < bi)) {
-        bp = op;
-        bi = oi;
-      }
-    }
+    wave_best_pair(bp, bi);
     if (lane == r) {
       my_p = bp;
       my_i = bi;

@@ -31,6 +31,18 @@ def test_topk_matches_oracle_with_ties(pkg, dev, n, k):
     assert np.array_equal(vals.cpu().numpy(), ref_v)
 
 
+@pytest.mark.parametrize("n,k", [(4096, 8), (300000, 16), (70, 16), (130, 8)])
+def test_topk_constant_and_sparse(pkg, dev, n, k):
+    """All-equal values leave thousands of pairs at the block threshold (the
+    per-wave fallback); small n leaves most waves empty (no threshold)."""
+    for v in (torch.full((n,), 3.0, device=dev), torch.arange(n, device=dev).float() % 7):
+        ids, vals = pkg.topk_f32(v, k)
+        torch.cuda.synchronize()
+        ref_i, ref_v = oracle.lm_head_topk(v.cpu().numpy(), k)
+        assert np.array_equal(ids.cpu().numpy(), ref_i)
+        assert np.array_equal(vals.cpu().numpy(), ref_v)
+
+
 def test_topk_distinct_and_infinite(pkg, dev):
     v = torch.randn(300000, device=dev)
     v[::7] = -float("inf")
