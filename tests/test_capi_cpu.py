@@ -131,3 +131,42 @@ def test_synthetic_distributions(pkg):
     p = torch.exp(b.double())
     assert abs(float(p.sum()) - 1.0) < 1e-6  # f32 log-probabilities
     assert float(p.max() / p.min()) > 400  # 256^1.1 ~ 446
+
+
+def test_new_entry_point_validation(pkg):
+    """The multi-output FC, router FC, top-k, LM head, ingestion and routed
+    stack entry points reject bad arguments before any launch."""
+    L = pkg._lib
+    lib = L.lib()
+    p = C.c_void_p(1 << 20)
+    t = L.U4TensorC(1 << 20, 1 << 20, 1 << 20)
+    tens = (L.U4TensorC * 5)(*([t] * 5))
+    ns = (C.c_int64 * 5)(*([64] * 5))
+    ys = (C.c_void_p * 5)(*([1 << 20] * 5))
+    dts = (C.c_int32 * 5)(*([0] * 5))
+    assert lib.aima_u4_matvec_multi(p, 0, tens, ns, 2048, 128, ys, dts, None) == L.AIMA_E_INVALID
+    assert lib.aima_u4_matvec_multi(p, 5, tens, ns, 2048, 128, ys, dts, None) == L.AIMA_E_INVALID
+    bad_dt = (C.c_int32 * 5)(*([7] * 5))
+    assert lib.aima_u4_matvec_multi(p, 2, tens, ns, 2048, 128, ys, bad_dt, None) == L.AIMA_E_INVALID
+    assert lib.aima_u4_matvec_multi(p, 2, tens, ns, 3072, 128, ys, dts, None) == \
+        L.AIMA_E_UNSUPPORTED  # K not a power of two
+    assert lib.aima_router_fc_topk(p, C.byref(t), 2000, 2048, 128, 8, 1e-4, p, p, p, None) == \
+        L.AIMA_E_INVALID  # experts > 1024
+    assert lib.aima_router_fc_topk(p, C.byref(t), 256, 2048, 128, 17, 1e-4, p, p, p, None) == \
+        L.AIMA_E_INVALID  # k > 16
+    sz = C.c_size_t(0)
+    assert lib.aima_topk_workspace_size(1 << 21, 8, C.byref(sz)) == L.AIMA_E_INVALID
+    assert lib.aima_topk_workspace_size(248320, 8, C.byref(sz)) == L.AIMA_OK and sz.value > 0
+    assert lib.aima_topk_f32(p, 100, 0, p, p, None, 0, None) == L.AIMA_E_INVALID
+    assert lib.aima_topk_f32(p, 248320, 8, p, p, None, 0, None) == L.AIMA_E_INVALID  # no workspace
+    assert lib.aima_u4_lm_head_topk(p, p, p, p, 248320, 2048, 128, 8, p, p, p, None, 0, None) == \
+        L.AIMA_E_INVALID  # workspace too small
+    assert lib.aima_u4_group_major_to_rows(p, p, 3, 3, p, p, None) == L.AIMA_E_INVALID  # odd n*G
+    assert lib.aima_u4_rows_to_group_major(None, p, 4, 4, p, p, None) == L.AIMA_E_INVALID
+    assert lib.aima_q4k_unpack(p, 4, 300, p, p, p, None) == L.AIMA_E_INVALID  # cols % 256
+    lc = _fake_layer(pkg)
+    rt = (L.U4TensorC * 1)(t)
+    assert lib.aima_moe_stack_decode_routed(C.byref(lc), rt, 1, 1e-6, p, 8, 1e-4, p, p, p, p, 16,
+                                            None) == L.AIMA_E_WORKSPACE
+    assert lib.aima_moe_stack_decode_routed(C.byref(lc), rt, 1, 1e-6, p, 8, 0.0, p, p, p, p,
+                                            1 << 30, None) == L.AIMA_E_INVALID
