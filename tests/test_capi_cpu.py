@@ -170,3 +170,17 @@ def test_new_entry_point_validation(pkg):
                                             None) == L.AIMA_E_WORKSPACE
     assert lib.aima_moe_stack_decode_routed(C.byref(lc), rt, 1, 1e-6, p, 8, 0.0, p, p, p, p,
                                             1 << 30, None) == L.AIMA_E_INVALID
+
+
+def test_prefill_rejects_batches_past_the_offset_limit(pkg):
+    """tokens * (k + 1) * inter must stay below 2^30 f16 elements (32-bit byte
+    offsets in the grouped GEMM): 233,017 tokens at k = 8, inter = 512 is the
+    first batch refused."""
+    L = pkg._lib
+    lib = L.lib()
+    p = C.c_void_p(1 << 20)
+    lc = _fake_layer(pkg)
+    for T in (233017, 233018, 1 << 20):
+        rc = lib.aima_moe_grouped_prefill(C.byref(lc), p, None, T, p, p, 8, p, p, 1 << 40, None)
+        assert rc == L.AIMA_E_INVALID, T
+        assert b"2^30" in lib.aima_last_error()

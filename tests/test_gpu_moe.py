@@ -223,3 +223,22 @@ def test_decode_phases_compose(pkg, dev, layer_full):
     ref_act = np.concatenate([d["selected_swiglu"], d["shared_swiglu"]]).reshape(9, 512)
     assert_parity(f16_to_f32(act), ref_act, what="decode SwiGLU activations")
     assert abs(float(sigma.item()) - float(d["shared_gate"][1])) < 1e-5
+
+
+def test_prefill_largest_batch(pkg, dev, layer_full):
+    """T = 233016, the largest batch whose row offsets stay below 2^31 bytes
+    (tokens * (k + 1) * inter < 2^30 f16 elements at k = 8, inter = 512):
+    every token finite, sampled tokens against the oracle."""
+    layer, mw = layer_full
+    T = 233016
+    x = pkg.synth.activations(T, 2048, 77, dev)
+    ids, w = pkg.select_router_topk(pkg.synth.router_logits(T, 256, 78, dev), 8)
+    out = pkg.grouped_moe_prefill(layer, x, ids, w)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    sel = torch.tensor([0, 1, 116508, T - 2, T - 1], device=dev)
+    got = f16_to_f32(out[sel])
+    ref = oracle.moe_ffn_tokens(mw, f16_to_f32(x[sel]), ids[sel].cpu().numpy(),
+                                w[sel].cpu().numpy(), threads=THREADS)
+    assert_parity(got, ref, what="largest batch")
+    del out, x
