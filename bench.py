@@ -178,6 +178,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true",
                     help="only the headline decode step (for profiling runs)")
+    ap.add_argument("--prefill-tokens", type=int, default=2048,
+                    help="with --prefill-only: tokens of the one timed layer (2048 = config 2 "
+                         "with Zipf routing; other values use uniform routing, as config 4b)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the config 2 grouped prefill (one layer, T=2048), timed with "
                          "--steps launches; prints its JSON entry (for profiling runs)")
@@ -214,8 +217,10 @@ def main():
         layer = synth.moe_layer(hidden=H, inter=I, experts=E, group=GROUP, seed=4000, device=dev)
         layers_c = ops._layers_c([layer])
         res = prefill_config2(torch, pkg, ops, synth, layer, layers_c, dev, args.steps,
-                              args.warmup)
-        print(json.dumps({"prefill_config2_T2048": res}), flush=True)
+                              args.warmup, T=args.prefill_tokens)
+        key = ("prefill_config2_T2048" if args.prefill_tokens == 2048
+               else f"prefill_layer_T{args.prefill_tokens}_uniform")
+        print(json.dumps({key: res}), flush=True)
         return
     log(f"device {torch.cuda.get_device_name(0)}; building 40-layer stack")
     t0 = time.perf_counter()
@@ -319,11 +324,13 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def prefill_config2(torch, pkg, ops, synth, layer, layers_c, dev, iters=50, warmup=5):
-    """Config 2: one layer, T=2048, Zipf(1.1)-skewed routing."""
-    T = 2048
+def prefill_config2(torch, pkg, ops, synth, layer, layers_c, dev, iters=50, warmup=5,
+                    T=2048):
+    """Config 2: one layer, T=2048, Zipf(1.1)-skewed routing (another T: one
+    layer of that many tokens with uniform routing, as in config 4b)."""
     x = synth.activations(T, H, 2, dev)
-    ids, w = ops.select_router_topk(synth.router_logits(T, E, 3, dev, zipf_s=1.1), K_TOP)
+    ids, w = ops.select_router_topk(synth.router_logits(T, E, 3, dev,
+                                                        zipf_s=1.1 if T == 2048 else None), K_TOP)
     ws = ops.Workspace(dev)
     o = torch.empty_like(x)
 
@@ -348,7 +355,7 @@ def prefill_config2(torch, pkg, ops, synth, layer, layers_c, dev, iters=50, warm
            "hbm_weight_gbs": round(wbytes / us / 1e3, 1),
            "active_experts": active, "max_group": int(counts.max()),
            "flops": flops}
-    log(f"prefill T=2048: {us:.1f} us, {T / us * 1e6:.0f} tok/s, {tf:.1f} TFLOP/s")
+    log(f"prefill T={T}: {us:.1f} us, {T / us * 1e6:.0f} tok/s, {tf:.1f} TFLOP/s")
     return res
 
 
