@@ -17,6 +17,7 @@ from .ops import (  # noqa: F401
     apply_rms_norm,
     build_grouped_schedule,
     grouped_moe_prefill,
+    grouped_moe_prefill_routed,
     lm_head_topk,
     matvec_u4,
     matvec_u4_multi,
@@ -25,12 +26,14 @@ from .ops import (  # noqa: F401
     moe_stack_decode,
     moe_stack_decode_routed,
     moe_stack_prefill,
+    prefill_workspace_views,
     q4k_unpack,
     router_fc_topk,
     run_moe_ffn_layer,
     select_router_topk,
     topk_f32,
     u4_dequant,
+    u4_dequant_f16,
     u4_group_major_to_rows,
     u4_rows_to_group_major,
 )

@@ -28,6 +28,8 @@ AIMA_DEVERR_TIMEOUT = 4
 AIMA_OUT_F16 = 0
 AIMA_OUT_F32 = 1
 AIMA_MAX_MULTI_OUT = 4
+AIMA_PREFILL_FULL_F16 = 0
+AIMA_PREFILL_ROUTED_F32 = 1
 
 # Every symbol the header declares, with (restype, argtypes).
 _vp = C.c_void_p
@@ -45,7 +47,19 @@ class MoeLayerC(C.Structure):
     _fields_ = [("gate_up", U4TensorC), ("down", U4TensorC), ("shared_gate_up", U4TensorC),
                 ("shared_down", U4TensorC), ("shared_gate_vec", _vp), ("norm_weight", _vp),
                 ("hidden", _i32), ("inter", _i32), ("shared_inter", _i32),
-                ("experts", _i32), ("group", _i32)]
+                ("experts", _i32), ("group", _i32), ("up", U4TensorC),
+                ("shared_up", U4TensorC)]
+
+
+class PrefillOptionsC(C.Structure):
+    _fields_ = [("output_mode", _i32), ("input_f32", _i32), ("topk_stride", _i64),
+                ("stage_events", _vp * 5)]
+
+
+class PrefillViewsC(C.Structure):
+    _fields_ = [("offsets", _vp), ("token_map", _vp), ("inverse_map", _vp),
+                ("compact_weights", _vp), ("weighted_swiglu", _vp), ("contributions", _vp),
+                ("tiles", _vp), ("tile_count", _vp)]
 
 
 _LP = C.POINTER(MoeLayerC)
@@ -54,6 +68,7 @@ SIGNATURES = {
     "aima_last_error": (C.c_char_p, []),
     "aima_version": (C.c_int, []),
     "aima_u4_dequant": (C.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _vp, _vp]),
+    "aima_u4_dequant_f16": (C.c_int, [_vp, _vp, _vp, _i64, _i64, _i32, _vp, _vp]),
     "aima_u4_matvec": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _vp, _i32, _vp]),
     "aima_rmsnorm": (C.c_int, [_vp, _vp, _i64, _i64, _f32, _vp, _vp]),
     "aima_router_topk": (C.c_int, [_vp, _i64, _i32, _i32, _f32, _vp, _vp, _vp]),
@@ -76,6 +91,10 @@ SIGNATURES = {
     "aima_moe_prefill_workspace_size": (C.c_int, [_LP, _i64, _i32, _szp]),
     "aima_moe_grouped_prefill": (C.c_int, [_LP, _vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp,
                                            C.c_size_t, _vp]),
+    "aima_moe_grouped_prefill_ex": (C.c_int, [_LP, _vp, _vp, _i64, _vp, _vp, _i32, _vp,
+                                              C.POINTER(PrefillOptionsC), _vp, C.c_size_t, _vp]),
+    "aima_moe_prefill_workspace_views": (C.c_int, [_LP, _i64, _i32, _vp,
+                                                   C.POINTER(PrefillViewsC)]),
     "aima_grouped_schedule_workspace_size": (C.c_int, [_i64, _i32, _i32, _szp]),
     "aima_grouped_schedule": (C.c_int, [_vp, _vp, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
                                         C.c_size_t, _vp]),

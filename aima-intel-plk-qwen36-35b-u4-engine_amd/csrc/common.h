@@ -52,6 +52,55 @@ int launch_check(const char* what);
 // log2 of a supported group size (32, 64, 128, 256), else -1.
 int group_log2_of(int group);
 
+// Gate and up projections of an expert stack in either boundary form:
+//   concatenated: gate_up = E x [2I][H], up rows after the gate rows (the CPU
+//                 reference's convention, engine/src/gguf_loader.cpp:4654-4660);
+//   split:        gate = E x [I][H] and up = E x [I][H] (the OpenVINO
+//                 MOE3GemmFusedCompressed operands,
+//                 engine/openvino/iq36-fixed-fc-moe-router-compat.patch:49-56),
+//                 selected by a non-null up.qweight.
+// Projection h (0 gate, 1 up) of unit j of expert e is row row(e, h, j) of
+// tensor h; its scales and zero points are at the same flat row index.
+struct GateUpView {
+  const uint8_t* q[2];
+  const uint16_t* s[2];
+  const uint8_t* z[2];
+  int64_t expert_rows;  // rows per expert in each tensor (2I or I)
+  int64_t up_row0;      // first up row of an expert in tensor 1 (I or 0)
+  __host__ __device__ int64_t row(int64_t e, int h, int64_t j) const {
+    return e * expert_rows + (h ? up_row0 : 0) + j;
+  }
+};
+
+__host__ __device__ inline GateUpView gate_up_view(const aima_u4_tensor& gate_up, const aima_u4_tensor& up,
+                               int64_t inter) {
+  GateUpView v;
+  const bool split = up.qweight != nullptr;
+  v.q[0] = gate_up.qweight;
+  v.s[0] = gate_up.scale;
+  v.z[0] = gate_up.zp;
+  v.q[1] = split ? up.qweight : gate_up.qweight;
+  v.s[1] = split ? up.scale : gate_up.scale;
+  v.z[1] = split ? up.zp : gate_up.zp;
+  v.expert_rows = split ? inter : 2 * inter;
+  v.up_row0 = split ? 0 : inter;
+  return v;
+}
+__host__ __device__ inline GateUpView routed_gate_up(const aima_moe_layer& L) {
+  return gate_up_view(L.gate_up, L.up, L.inter);
+}
+__host__ __device__ inline GateUpView shared_gate_up(const aima_moe_layer& L) {
+  return gate_up_view(L.shared_gate_up, L.shared_up, L.shared_inter);
+}
+// Null checks and qweight alignment of the optional split up tensors.
+inline bool split_tensors_ok(const aima_moe_layer& L) {
+  auto ok = [](const aima_u4_tensor& t) {
+    return t.qweight == nullptr ? (t.scale == nullptr && t.zp == nullptr)
+                                : (t.scale != nullptr && t.zp != nullptr && aligned(t.qweight, 16));
+  };
+  return ok(L.up) && ok(L.shared_up);
+}
+
 // ---------------------------------------------------------------------------
 // device helpers
 // ---------------------------------------------------------------------------
@@ -227,6 +276,36 @@ __device__ __forceinline__ float u4_chunk_raw(const u32x4 w, const XChunk& c, ui
 __device__ __forceinline__ float u4_chunk_dot(const u32x4 w, const XChunk& c, uint32_t z,
                                               float s, uint32_t magic) {
   return (u4_chunk_raw(w, c, magic) - c.bias - (float)z * c.xsum) * s;
+}
+
+// ---------------------------------------------------------------------------
+// f16 dequantization of 8 nibbles (the MFMA operand of the grouped GEMM).
+//
+// One 32-bit word holds k0..k7; the result is f16((q - z) * s) for k0..k7 in
+// natural order (k0,k1),(k2,k3),(k4,k5),(k6,k7).  A byte permute puts byte i
+// of the word in bits 0..7 and byte i of (word >> 4) in bits 16..23, so the
+// mask 0x000F000F leaves (q_2i, q_2i+1) in the two halves; OR-ing 0x6400
+// makes each half the f16 value 1024 + q exactly.  Subtracting zz2 =
+// {1024 + z, 1024 + z} is exact ((q - z) is an integer in [-15, 15]) and the
+// product with ss2 = {s, s} is the one rounding: the result equals
+// f16(f32(q - z) * f32(s)) for every f16 scale, subnormals included (both
+// halves use the scale itself, never a rescaled copy of it).  `magic` is
+// 0x64006400 in a VGPR (see u4_magic).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f16x2 u4_zz2(uint32_t z) {
+  return as_h2((0x6400u | z) * 0x00010001u);
+}
+__device__ __forceinline__ f16x2 u4_ss2(uint32_t scale_bits) {
+  return as_h2((scale_bits & 0xffffu) * 0x00010001u);
+}
+__device__ __forceinline__ f16x8 dequant8(uint32_t d, f16x2 zz2, f16x2 ss2, uint32_t magic) {
+  const uint32_t d4 = d >> 4;
+  const f16x2 p0 = (as_h2((__builtin_amdgcn_perm(d4, d, 0x0C040C00u) & 0x000F000Fu) | magic) - zz2) * ss2;
+  const f16x2 p1 = (as_h2((__builtin_amdgcn_perm(d4, d, 0x0C050C01u) & 0x000F000Fu) | magic) - zz2) * ss2;
+  const f16x2 p2 = (as_h2((__builtin_amdgcn_perm(d4, d, 0x0C060C02u) & 0x000F000Fu) | magic) - zz2) * ss2;
+  const f16x2 p3 = (as_h2((__builtin_amdgcn_perm(d4, d, 0x0C070C03u) & 0x000F000Fu) | magic) - zz2) * ss2;
+  const u32x4 v{h2_bits(p0), h2_bits(p1), h2_bits(p2), h2_bits(p3)};
+  return __builtin_bit_cast(f16x8, v);
 }
 
 // Loads through pointers the compiler cannot prove global (e.g. read from a

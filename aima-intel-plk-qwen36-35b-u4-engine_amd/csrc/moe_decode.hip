@@ -124,36 +124,41 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
   // the block's slot (inter is a multiple of BP: every block lies in one slot)
   const int64_t slot = bpair0 / I;
   const int64_t j0 = bpair0 - slot * I;
-  const int64_t rows_e = 2 * I;
-  const uint8_t* qw;
-  const uint16_t* sc;
-  const uint8_t* zp;
+  // the block's gate run (h = 0) and up run (h = 1): rows j0 .. j0 + BP - 1
+  // of the expert's gate and up projections, either boundary form
+  const uint8_t* qw[2];
+  const uint16_t* sc[2];
+  const uint8_t* zp[2];
   bool valid = bpair0 < total_pairs;
-  if (slot < k) {
-    const int32_t e = valid ? ids[slot] : 0;
-    if (valid && (e < 0 || e >= L.experts)) {
-      if (j0 == 0 && threadIdx.x == 0) atomicOr(err, AIMA_DEVERR_EXPERT_RANGE);
-      valid = false;
+  {
+    int64_t ee = 0;
+    if (slot < k) {
+      const int32_t e = valid ? ids[slot] : 0;
+      if (valid && (e < 0 || e >= L.experts)) {
+        if (j0 == 0 && threadIdx.x == 0) atomicOr(err, AIMA_DEVERR_EXPERT_RANGE);
+        valid = false;
+      }
+      ee = valid ? e : 0;
     }
-    const int64_t ee = valid ? e : 0;
-    qw = L.gate_up.qweight + ee * rows_e * (G::K / 2);
-    sc = L.gate_up.scale + ee * rows_e * groups;
-    zp = L.gate_up.zp + ee * (rows_e * groups / 2);
-  } else {
-    qw = L.shared_gate_up.qweight;
-    sc = L.shared_gate_up.scale;
-    zp = L.shared_gate_up.zp;
+    const GateUpView V = slot < k ? routed_gate_up(L) : shared_gate_up(L);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t r0 = V.row(ee, h, j0);
+      qw[h] = V.q[h] + r0 * (G::K / 2);
+      sc[h] = V.s[h] + r0 * groups;
+      zp[h] = V.z[h] + ((r0 * groups) >> 1);  // r0 * groups is even (j0 % 8 == 0)
+    }
   }
   // weights first: they stream while the activation operands are built
   u32x4 w[PASSES][G::NC];
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
     const int ri = ps * G::RPI + seg;  // row index in this wave's list
-    const int64_t row = ((ri & 1) ? I : 0) + j0 + wave * kPairsPerWave + ri / 2;
+    const int64_t row = wave * kPairsPerWave + ri / 2;  // within the block's run
 #pragma unroll
     for (int i = 0; i < G::NC; ++i) {
       const int c = cl + i * G::SEG;
-      w[ps][i] = (valid && ri < NR) ? load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16)
+      w[ps][i] = (valid && ri < NR) ? load16_nt(qw[ri & 1] + row * (G::K / 2) + (int64_t)c * 16)
                                     : u32x4{0u, 0u, 0u, 0u};
     }
   }
@@ -161,11 +166,11 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
     const int n = BP * groups;  // scales per run
     for (int t = threadIdx.x; t < 2 * n; t += 256) {
       const int up = t >= n;
-      s_lds[t] = sc[((up ? I : 0) + j0) * groups + (t - up * n)];
+      s_lds[t] = sc[up][t - up * n];
     }
     for (int t = threadIdx.x; t < n; t += 256) {
       const int up = t >= n / 2;
-      z_lds[up][t - up * (n / 2)] = zp[(((up ? I : 0) + j0) * groups >> 1) + (t - up * (n / 2))];
+      z_lds[up][t - up * (n / 2)] = zp[up][t - up * (n / 2)];
     }
   }
   XChunk xc[G::NC];
@@ -355,6 +360,8 @@ static int check_layer(const aima_moe_layer* L, int k, bool need_norm) {
   AIMA_REQUIRE(aligned(L->gate_up.qweight, 16) && aligned(L->down.qweight, 16) &&
                    aligned(L->shared_gate_up.qweight, 16) && aligned(L->shared_down.qweight, 16),
                "moe: qweight pointers must be 16-byte aligned");
+  AIMA_REQUIRE(split_tensors_ok(*L),
+               "moe: a split up tensor needs qweight, scale and zp (qweight 16-byte aligned)");
   return AIMA_OK;
 }
 

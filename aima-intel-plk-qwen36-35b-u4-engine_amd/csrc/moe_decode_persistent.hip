@@ -48,6 +48,7 @@
 #include <math.h>
 
 #include <string>
+#include <vector>
 
 namespace aima {
 
@@ -80,8 +81,34 @@ static_assert(kPairs % 3 == 0, "blocks own whole act records");
 static_assert(kActRecords <= 192, "the activation poll covers records 0..191");
 static_assert(kRowsB % kWaves == 0 && kWaveRowsB == 8, "8 output rows per wave");
 
+// One layer's tensors, resolved on the host for the kernel: the routed gate
+// (h = 0) and up (h = 1) projections as their expert-0, unit-0 rows plus a
+// byte stride per expert (either boundary form of aima_moe_layer: the
+// concatenated gate_up has the up rows I rows after the gate rows, the split
+// form two tensors), the shared expert's gate/up at unit 0, both down
+// projections, the shared gate vector and the RMSNorm weight.
+struct PlanLayer {
+  const uint8_t* gq[2];
+  const uint16_t* gs[2];
+  const uint8_t* gz[2];
+  const uint8_t* sq[2];
+  const uint16_t* ss[2];
+  const uint8_t* sz[2];
+  const uint8_t* dq;
+  const uint16_t* ds;
+  const uint8_t* dz;
+  const uint8_t* sdq;
+  const uint16_t* sds;
+  const uint8_t* sdz;
+  const uint16_t* gate_vec;
+  const float* norm;
+  uint32_t estride_q, estride_s, estride_z;  // routed gate/up bytes per expert
+  uint32_t pad;
+};
+static_assert(sizeof(PlanLayer) % 4 == 0, "the table is copied as 32-bit words");
+
 struct PersistArgs {
-  const aima_moe_layer* layers;   // device table [n_layers]
+  const PlanLayer* layers;        // device table [n_layers]
   int n_layers;
   int k;
   int experts;
@@ -176,7 +203,7 @@ struct SharedState {
   float ss[kWaves];                    // per-wave sums of squares of r_L
   float gp[kWaves];                    // per-wave shared-gate partial dots
   float rowsum[kRowsA];
-  aima_moe_layer table[kMaxLayers];    // the layer table, copied once
+  PlanLayer table[kMaxLayers];         // the layer table, copied once
   int32_t route_id[kMaxLayers][kMaxK];
   float route_w[kMaxLayers][kMaxK];
   float sigma;
@@ -376,7 +403,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   {
     const uint32_t* src = reinterpret_cast<const uint32_t*>(a.layers);
     uint32_t* dst = reinterpret_cast<uint32_t*>(S.table);
-    const int words = a.n_layers * (int)(sizeof(aima_moe_layer) / 4);
+    const int words = a.n_layers * (int)(sizeof(PlanLayer) / 4);
     for (int i = threadIdx.x; i < words; i += kThreads) dst[i] = src[i];
   }
   // block 0 advances the launch counter on every exit path
@@ -525,10 +552,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // 0..4 (lanes above repeat lane 49)
   auto gather_a = [&](int L) {
     const int ln = opaque_v(threadIdx.x & 63);
-    const aima_moe_layer& Ly = S.table[L];
+    const PlanLayer& Ly = S.table[L];
     const uint32_t e = slot_expert(L);
-    const uint32_t sbytes = (uint32_t)(2 * kI) * 16 * 2;
-    const uint32_t zbytes = (uint32_t)(2 * kI) * 16 / 2;
     const int q = min(ln, 49);
     const bool is_s = q < 40;
     const int i = is_s ? (q >> 3) : ((q - 40) >> 1);
@@ -537,13 +562,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     const int p = j * kPairs + (ri >> 1);
     const bool routed = p < kI;
     const int unit = routed ? p : x * kSlice + (p - kI);
-    const int row = (ri & 1) ? kI + unit : unit;
-    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.gate_up.scale) + (size_t)e * sbytes;
-    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.gate_up.zp) + (size_t)e * zbytes;
-    const AIMA_GLOBAL uint8_t* hs = uptr(Ly.shared_gate_up.scale);
-    const AIMA_GLOBAL uint8_t* hz = uptr(Ly.shared_gate_up.zp);
+    const bool up = (ri & 1) != 0;
+    const AIMA_GLOBAL uint8_t* rs0 = uptr(Ly.gs[0]) + (size_t)e * Ly.estride_s;
+    const AIMA_GLOBAL uint8_t* rs1 = uptr(Ly.gs[1]) + (size_t)e * Ly.estride_s;
+    const AIMA_GLOBAL uint8_t* rz0 = uptr(Ly.gz[0]) + (size_t)e * Ly.estride_z;
+    const AIMA_GLOBAL uint8_t* rz1 = uptr(Ly.gz[1]) + (size_t)e * Ly.estride_z;
+    const AIMA_GLOBAL uint8_t* hs = up ? uptr(Ly.ss[1]) : uptr(Ly.ss[0]);
+    const AIMA_GLOBAL uint8_t* hz = up ? uptr(Ly.sz[1]) : uptr(Ly.sz[0]);
+    const AIMA_GLOBAL uint8_t* rs = up ? rs1 : rs0;
+    const AIMA_GLOBAL uint8_t* rz = up ? rz1 : rz0;
     const AIMA_GLOBAL uint8_t* base = is_s ? (routed ? rs : hs) : (routed ? rz : hz);
-    const uint32_t off = is_s ? (uint32_t)row * 32 + 4 * w : (uint32_t)row * 8 + 4 * w;
+    const uint32_t off = is_s ? (uint32_t)unit * 32 + 4 * w : (uint32_t)unit * 8 + 4 * w;
     gsa_n = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
   };
   // down gather (4 groups per row; the wave's 8 rows are consecutive):
@@ -551,16 +580,16 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // 20..35 = shared scale words, 36..39 = shared zero-point words
   auto gather_b = [&](int L) {
     const int ln = opaque_v(threadIdx.x & 63);
-    const aima_moe_layer& Ly = S.table[L];
+    const PlanLayer& Ly = S.table[L];
     const uint32_t e = slot_expert(L);
     const uint32_t sbytes = (uint32_t)kH * 4 * 2;
     const uint32_t zbytes = (uint32_t)kH * 4 / 2;
     const uint32_t h0 = (uint32_t)(j * kRowsB + wave * kWaveRowsB);
     const int q = min(ln, 39);
-    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.down.scale) + (size_t)e * sbytes;
-    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.down.zp) + (size_t)e * zbytes;
-    const AIMA_GLOBAL uint8_t* hs = uptr(Ly.shared_down.scale);
-    const AIMA_GLOBAL uint8_t* hz = uptr(Ly.shared_down.zp);
+    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.ds) + (size_t)e * sbytes;
+    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.dz) + (size_t)e * zbytes;
+    const AIMA_GLOBAL uint8_t* hs = uptr(Ly.sds);
+    const AIMA_GLOBAL uint8_t* hz = uptr(Ly.sdz);
     const AIMA_GLOBAL uint8_t* base = q < 16 ? rs : q < 20 ? rz : q < 36 ? hs : hz;
     const uint32_t off = q < 16   ? h0 * 8 + 4 * q
                          : q < 20 ? h0 * 2 + 4 * (q - 16)
@@ -575,24 +604,21 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // the block's last row).
   auto prefetch_a1 = [&](int L, int i) {
     const int ln = opaque_v(threadIdx.x & 63);
-    const aima_moe_layer& Ly = S.table[L];
+    const PlanLayer& Ly = S.table[L];
     const uint32_t e = slot_expert(L);
-    const uint32_t wbytes = (uint32_t)(2 * kI) * (kH / 2);
-    const uint32_t sbytes = (uint32_t)(2 * kI) * gA * 2;
-    const uint32_t zbytes = (uint32_t)(2 * kI) * gA / 2;
     const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
+    const int h = ri & 1;
     const int p = j * kPairs + (ri >> 1);
     const bool routed = p < kI;
-    const AIMA_GLOBAL uint8_t* w = routed ? uptr(Ly.gate_up.qweight) + (size_t)e * wbytes
-                                          : uptr(Ly.shared_gate_up.qweight);
-    const AIMA_GLOBAL uint8_t* sp = routed ? uptr(Ly.gate_up.scale) + (size_t)e * sbytes
-                                           : uptr(Ly.shared_gate_up.scale);
-    const AIMA_GLOBAL uint8_t* zp = routed ? uptr(Ly.gate_up.zp) + (size_t)e * zbytes
-                                           : uptr(Ly.shared_gate_up.zp);
+    const AIMA_GLOBAL uint8_t* w = routed ? uptr(Ly.gq[h]) + (size_t)e * Ly.estride_q
+                                          : uptr(Ly.sq[h]);
+    const AIMA_GLOBAL uint8_t* sp = routed ? uptr(Ly.gs[h]) + (size_t)e * Ly.estride_s
+                                           : uptr(Ly.ss[h]);
+    const AIMA_GLOBAL uint8_t* zp = routed ? uptr(Ly.gz[h]) + (size_t)e * Ly.estride_z
+                                           : uptr(Ly.sz[h]);
     const int unit = routed ? p : x * kSlice + (p - kI);
-    const int row = (ri & 1) ? kI + unit : unit;
-    const int gi = row * gA + ((ln * 32) >> glog2);
-    wa_n[i] = ld_w(w, (uint32_t)row * (kH / 2) + ln * 16);
+    const int gi = unit * gA + ((ln * 32) >> glog2);
+    wa_n[i] = ld_w(w, (uint32_t)unit * (kH / 2) + ln * 16);
     if (g128) {
       if (i == 0) gather_a(L);
     } else {
@@ -601,47 +627,22 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     }
   };
   auto prefetch_a = [&](int L) {
-    const int ln = opaque_v(threadIdx.x & 63);
-    const aima_moe_layer& Ly = S.table[L];
-    const uint32_t e = slot_expert(L);
-    const uint32_t wbytes = (uint32_t)(2 * kI) * (kH / 2);      // per expert
-    const uint32_t sbytes = (uint32_t)(2 * kI) * gA * 2;
-    const uint32_t zbytes = (uint32_t)(2 * kI) * gA / 2;
-    const AIMA_GLOBAL uint8_t* rw = uptr(Ly.gate_up.qweight) + (size_t)e * wbytes;
-    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.gate_up.scale) + (size_t)e * sbytes;
-    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.gate_up.zp) + (size_t)e * zbytes;
-    const AIMA_GLOBAL uint8_t* hw = uptr(Ly.shared_gate_up.qweight);
-    const AIMA_GLOBAL uint8_t* hs = uptr(Ly.shared_gate_up.scale);
-    const AIMA_GLOBAL uint8_t* hz = uptr(Ly.shared_gate_up.zp);
 #pragma unroll
-    for (int i = 0; i < kMaxRowsA; ++i) {
-      const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
-      const int p = j * kPairs + (ri >> 1);  // pair within the XCD
-      const bool routed = p < kI;
-      const int unit = routed ? p : x * kSlice + (p - kI);
-      const int row = (ri & 1) ? kI + unit : unit;
-      const int gi = row * gA + ((ln * 32) >> glog2);
-      wa_n[i] = ld_w(routed ? rw : hw, (uint32_t)row * (kH / 2) + ln * 16);
-      if (!g128) {
-        sa_n[i] = ld_u32(routed ? rs : hs, (gi * 2) & ~3);
-        za_n[i] = ld_u32(routed ? rz : hz, (gi >> 1) & ~3);
-      }
-    }
-    if (g128) gather_a(L);
+    for (int i = 0; i < kMaxRowsA; ++i) prefetch_a1(L, i);
   };
   // down rows: wave w owns block rows 8w .. 8w+7; units 0, 1 = routed rows
   // 4u + (lane >> 4), chunk lane & 15; unit 2 = the shared slice, row
   // (lane & 15) >> 1, chunk 2x + (lane & 1) of the full shared row
   auto prefetch_b = [&](int L) {
     const int ln = opaque_v(threadIdx.x & 63);
-    const aima_moe_layer& Ly = S.table[L];
+    const PlanLayer& Ly = S.table[L];
     const uint32_t e = slot_expert(L);
     const uint32_t wbytes = (uint32_t)kH * (kI / 2);
     const uint32_t sbytes = (uint32_t)kH * gB * 2;
     const uint32_t zbytes = (uint32_t)kH * gB / 2;
-    const AIMA_GLOBAL uint8_t* rw = uptr(Ly.down.qweight) + (size_t)e * wbytes;
-    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.down.scale) + (size_t)e * sbytes;
-    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.down.zp) + (size_t)e * zbytes;
+    const AIMA_GLOBAL uint8_t* rw = uptr(Ly.dq) + (size_t)e * wbytes;
+    const AIMA_GLOBAL uint8_t* rs = uptr(Ly.ds) + (size_t)e * sbytes;
+    const AIMA_GLOBAL uint8_t* rz = uptr(Ly.dz) + (size_t)e * zbytes;
     const int h0 = j * kRowsB + wave * kWaveRowsB;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -658,10 +659,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       const int row = h0 + ((ln & 15) >> 1);
       const int ch = 2 * x + (ln & 1);
       const int gi = row * gB + ((ch * 32) >> glog2);
-      wb_n[2] = ld_w(uptr(Ly.shared_down.qweight), (uint32_t)row * (kI / 2) + ch * 16);
+      wb_n[2] = ld_w(uptr(Ly.sdq), (uint32_t)row * (kI / 2) + ch * 16);
       if (!g128) {
-        sb_n[2] = ld_u32(uptr(Ly.shared_down.scale), (gi * 2) & ~3);
-        zb_n[2] = ld_u32(uptr(Ly.shared_down.zp), (gi >> 1) & ~3);
+        sb_n[2] = ld_u32(uptr(Ly.sds), (gi * 2) & ~3);
+        zb_n[2] = ld_u32(uptr(Ly.sdz), (gi >> 1) & ~3);
       }
     }
     if (g128) gather_b(L);
@@ -670,10 +671,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // values 256 w + 4 l .. +3
   auto load_vec = [&](int L) {
     const int ln = opaque_v(threadIdx.x & 63);
-    const aima_moe_layer& Ly = S.table[L];
+    const PlanLayer& Ly = S.table[L];
     const int v0 = wave * 256 + ln * 4;
-    nw_n = gload16(Ly.norm_weight + v0);
-    gv_n = *reinterpret_cast<const AIMA_GLOBAL u32x2*>(uptr(Ly.shared_gate_vec) + v0 * 2);
+    nw_n = gload16(Ly.norm + v0);
+    gv_n = *reinterpret_cast<const AIMA_GLOBAL u32x2*>(uptr(Ly.gate_vec) + v0 * 2);
   };
 
   load_vec(0);
@@ -831,8 +832,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
         if (ri < kRowsA) {
           const int p = j * kPairs + (ri >> 1);
           const int unit = p < kI ? p : x * kSlice + (p - kI);
-          const int row = (ri & 1) ? kI + unit : unit;
-          const int gi = row * gA + ((ln * 32) >> glog2);
+          const int gi = unit * gA + ((ln * 32) >> glog2);
           const float dd =
               segment_sum<64>(u4_chunk_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
           if (lane == 0) S.rowsum[ri] = dd;
@@ -1027,7 +1027,7 @@ struct aima_moe_decode_plan {
   int group_log2 = 0;
   int blocks = 0;
   char* mem = nullptr;  // device allocation holding everything below
-  aima_moe_layer* table = nullptr;
+  PlanLayer* table = nullptr;
   uint32_t* rx = nullptr;
   uint64_t* actx = nullptr;
   uint64_t* pbuf = nullptr;
@@ -1064,14 +1064,55 @@ int persistent_shape_ok(const aima_moe_layer* layers, int n, int k, std::string*
       *why = "null tensor pointer";
       return 0;
     }
+    if (!split_tensors_ok(L)) {
+      *why = "a split up tensor needs qweight, scale and zp";
+      return 0;
+    }
     if (!aligned(L.gate_up.qweight, 16) || !aligned(L.down.qweight, 16) ||
         !aligned(L.shared_gate_up.qweight, 16) || !aligned(L.shared_down.qweight, 16) ||
         !aligned(L.shared_gate_vec, 16) || !aligned(L.norm_weight, 16)) {
       *why = "qweight, shared_gate_vec and norm_weight must be 16-byte aligned";
       return 0;
     }
+    // scales and zero points are read as 32-bit words
+    const aima_u4_tensor* ts[] = {&L.gate_up, &L.down, &L.shared_gate_up, &L.shared_down,
+                                  &L.up, &L.shared_up};
+    for (const aima_u4_tensor* t : ts) {
+      if (t->qweight && (!aligned(t->scale, 4) || !aligned(t->zp, 4))) {
+        *why = "scale and zp pointers must be 4-byte aligned";
+        return 0;
+      }
+    }
   }
   return 1;
+}
+
+// The kernel's table entry of one layer (shapes already validated).
+PlanLayer plan_layer(const aima_moe_layer& L) {
+  const int64_t G = L.hidden / L.group;  // groups per gate/up row
+  const GateUpView r = routed_gate_up(L), s = shared_gate_up(L);
+  PlanLayer p{};
+  for (int h = 0; h < 2; ++h) {
+    const int64_t r0 = r.row(0, h, 0), s0 = s.row(0, h, 0);
+    p.gq[h] = r.q[h] + r0 * (L.hidden / 2);
+    p.gs[h] = r.s[h] + r0 * G;
+    p.gz[h] = r.z[h] + r0 * G / 2;
+    p.sq[h] = s.q[h] + s0 * (L.hidden / 2);
+    p.ss[h] = s.s[h] + s0 * G;
+    p.sz[h] = s.z[h] + s0 * G / 2;
+  }
+  p.estride_q = (uint32_t)(r.expert_rows * (L.hidden / 2));
+  p.estride_s = (uint32_t)(r.expert_rows * G * 2);
+  p.estride_z = (uint32_t)(r.expert_rows * G / 2);
+  p.dq = L.down.qweight;
+  p.ds = L.down.scale;
+  p.dz = L.down.zp;
+  p.sdq = L.shared_down.qweight;
+  p.sds = L.shared_down.scale;
+  p.sdz = L.shared_down.zp;
+  p.gate_vec = L.shared_gate_vec;
+  p.norm = L.norm_weight;
+  return p;
 }
 
 }  // namespace
@@ -1109,7 +1150,7 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
     return at;
   };
   const size_t o_err = take(kWsHeader);
-  const size_t o_table = take(sizeof(aima_moe_layer) * n_layers);
+  const size_t o_table = take(sizeof(PlanLayer) * n_layers);
   const size_t o_rx = take(sizeof(uint32_t) * kXcds * 2 * kH);
   const size_t o_act = take(sizeof(uint64_t) * kXcds * 2 * kActStride);
   const size_t o_p = take(sizeof(uint64_t) * 2 * kH * kXcds);
@@ -1129,7 +1170,7 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
     return hip_check(e, "hipMalloc(decode plan)");
   }
   p->err = reinterpret_cast<uint32_t*>(p->mem + o_err);
-  p->table = reinterpret_cast<aima_moe_layer*>(p->mem + o_table);
+  p->table = reinterpret_cast<PlanLayer*>(p->mem + o_table);
   p->rx = reinterpret_cast<uint32_t*>(p->mem + o_rx);
   p->actx = reinterpret_cast<uint64_t*>(p->mem + o_act);
   p->pbuf = reinterpret_cast<uint64_t*>(p->mem + o_p);
@@ -1138,7 +1179,9 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   p->counter = reinterpret_cast<uint32_t*>(p->mem + o_ctr);
   e = hipMemset(p->mem, 0, off);
   if (e == hipSuccess) {
-    e = hipMemcpy(p->table, layers, sizeof(aima_moe_layer) * n_layers, hipMemcpyHostToDevice);
+    std::vector<PlanLayer> host(n_layers);
+    for (int l = 0; l < n_layers; ++l) host[l] = plan_layer(layers[l]);
+    e = hipMemcpy(p->table, host.data(), sizeof(PlanLayer) * n_layers, hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) {
     (void)hipFree(p->mem);

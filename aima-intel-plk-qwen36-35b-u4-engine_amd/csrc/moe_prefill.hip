@@ -48,6 +48,7 @@ struct PrefillWs {
   float* row_weight;     // [A]
   uint16_t* act;         // [A + T][I] f16
   uint16_t* contrib;     // [A + T][H] f16
+  uint16_t* x16;         // [T][H] f16 copy of an f32 input (layer calls)
   uint16_t* h;           // [T][H]   (stack only)
   uint16_t* r[2];        // [T][H]   (stack only)
   float* sigma[2];       // [T]      (stack only: shared-expert gates, by layer parity)
@@ -96,6 +97,7 @@ static size_t prefill_ws_layout(const PrefillDims& d, WsMode mode, void* base, P
   if (mode != WsMode::kSchedule) {
     l.act = reinterpret_cast<uint16_t*>(take((size_t)(d.A + d.T) * d.I * 2));
     l.contrib = reinterpret_cast<uint16_t*>(take((size_t)(d.A + d.T) * d.H * 2));
+    l.x16 = reinterpret_cast<uint16_t*>(take((size_t)d.T * d.H * 2));
   }
   if (mode == WsMode::kStack) {
     l.h = reinterpret_cast<uint16_t*>(take((size_t)d.T * d.H * 2));
@@ -127,13 +129,20 @@ __device__ __forceinline__ uint64_t match_mask(int e, uint64_t active, int bits)
   return m;
 }
 
+// The top-k ids of token t start at ids + t * stride (stride in int32 words,
+// >= k): RunLayer's byte topk_stride (grouped_s8_u4_prefill_runtime.hpp:62-84).
+__device__ __forceinline__ int32_t topk_id(const int32_t* __restrict__ ids, int32_t a, int k,
+                                           int stride) {
+  return ids[(int64_t)(a / k) * stride + a % k];
+}
+
 // One thread per assignment.  Validates the id (range, duplicate among the
 // earlier ranks of its token), ranks it among the block's assignments of the
 // same expert in assignment order (ballot match inside each wave plus the
 // counts of the earlier waves), and writes the block's per-expert counts.
 // The local rank is parked in inverse_map until the scatter.
 __global__ __launch_bounds__(kSchedBlock) void sched_count_kernel(
-    const int32_t* __restrict__ ids, int32_t A, int k, int E, int bits, uint32_t* err,
+    const int32_t* __restrict__ ids, int stride, int32_t A, int k, int E, int bits, uint32_t* err,
     int32_t* __restrict__ block_counts, int32_t* __restrict__ local_rank) {
   __shared__ int cnt[kSchedBlock / 64][kMaxExperts];
   __shared__ int32_t sid[16 + kSchedBlock];
@@ -146,7 +155,7 @@ __global__ __launch_bounds__(kSchedBlock) void sched_count_kernel(
   // starts in the previous block)
   for (int i = tid; i < 16 + kSchedBlock; i += kSchedBlock) {
     const int32_t a = base - 16 + i;
-    sid[i] = (a >= 0 && a < A) ? ids[a] : -1;
+    sid[i] = (a >= 0 && a < A) ? topk_id(ids, a, k, stride) : -1;
   }
   __syncthreads();
   const int32_t a = base + tid;
@@ -237,7 +246,8 @@ __device__ __forceinline__ int tiles_in_class(int total, int c) {
 // into row offsets and into tile positions per class (class 8 first).
 __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ block_base,
                                                           int32_t nb, int E, int Ep, int32_t T,
-                                                          int32_t A, int32_t* __restrict__ offsets,
+                                                          int32_t A, int with_shared,
+                                                          int32_t* __restrict__ offsets,
                                                           int32_t* __restrict__ tiles,
                                                           int32_t* __restrict__ tile_count) {
   __shared__ int smem[17 * (1 + kTileClasses)];
@@ -298,7 +308,7 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
 #pragma unroll
   for (int c = kTileClasses; c >= 1; --c) {
     cbase[c] = all_tiles;
-    all_tiles += tot[c] + tiles_in_class(T, c);
+    all_tiles += tot[c] + (with_shared ? tiles_in_class(T, c) : 0);
   }
   auto place = [&](int ex, int row_begin, int rows_total, int first8, int rem_pos_if_not8) {
     const int full = rows_total / kBM, rem = rows_total % kBM;
@@ -329,7 +339,7 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
   };
   if (rep) place(e, begin, total, cbase[kTileClasses] + v[kTileClasses], rem_slot(total, v));
   if (tid == 0) {
-    place(E, A, T, cbase[kTileClasses] + tot[kTileClasses], rem_slot(T, tot));
+    if (with_shared) place(E, A, T, cbase[kTileClasses] + tot[kTileClasses], rem_slot(T, tot));
     *tile_count = all_tiles;
   }
 }
@@ -337,12 +347,12 @@ __global__ __launch_bounds__(1024) void sched_scan_kernel(int32_t* __restrict__ 
 // One thread per assignment: the row = block base of its expert + its local
 // rank.
 __global__ __launch_bounds__(kSchedBlock) void sched_scatter_kernel(
-    const int32_t* __restrict__ ids, const float* __restrict__ weights, int32_t A, int k, int E,
-    const int32_t* __restrict__ block_base, int32_t* __restrict__ token_map,
+    const int32_t* __restrict__ ids, int stride, const float* __restrict__ weights, int32_t A,
+    int k, int E, const int32_t* __restrict__ block_base, int32_t* __restrict__ token_map,
     int32_t* __restrict__ inverse_map, float* __restrict__ row_weight) {
   const int32_t a = (int32_t)blockIdx.x * kSchedBlock + threadIdx.x;
   if (a >= A) return;
-  const int raw = ids[a];
+  const int raw = topk_id(ids, a, k, stride);
   const int e = (raw < 0 || raw >= E) ? 0 : raw;
   const int pos = block_base[(int64_t)blockIdx.x * E + e] + inverse_map[a];
   token_map[pos] = a / k;
@@ -353,21 +363,9 @@ __global__ __launch_bounds__(kSchedBlock) void sched_scatter_kernel(
 // ---------------------------------------------------------------------------
 // grouped GEMM
 // ---------------------------------------------------------------------------
-// 8 nibbles k0..k7 of one 32-bit word -> f16 (q - z) * s in natural order
-// (k0,k1),(k2,k3),(k4,k5),(k6,k7).  A byte permute copies byte i to bytes 0
-// and 2; masking 0x00F0000F leaves the even nibble as 1024 + q (low half) and
-// the odd one as 1024 + 16 q (high half), which use zz2 = {1024+z, 1024+16z}
-// and ss2 = {s, s/16}.  (q - z) is exact in f16 and (q - z) * s is rounded
-// once (relative error <= 2^-11), which keeps the group scale out of the f32
-// accumulators.  `magic` is 0x64006400 in a VGPR (one v_and_or_b32 per pair).
-__device__ __forceinline__ f16x8 dequant8(uint32_t d, f16x2 zz2, f16x2 ss2, uint32_t magic) {
-  const f16x2 p0 = (as_h2((__builtin_amdgcn_perm(d, d, 0x0C000C00u) & 0x00F0000Fu) | magic) - zz2) * ss2;
-  const f16x2 p1 = (as_h2((__builtin_amdgcn_perm(d, d, 0x0C010C01u) & 0x00F0000Fu) | magic) - zz2) * ss2;
-  const f16x2 p2 = (as_h2((__builtin_amdgcn_perm(d, d, 0x0C020C02u) & 0x00F0000Fu) | magic) - zz2) * ss2;
-  const f16x2 p3 = (as_h2((__builtin_amdgcn_perm(d, d, 0x0C030C03u) & 0x00F0000Fu) | magic) - zz2) * ss2;
-  const u32x4 v{h2_bits(p0), h2_bits(p1), h2_bits(p2), h2_bits(p3)};
-  return __builtin_bit_cast(f16x8, v);
-}
+// The weights enter the MFMAs as f16 (q - z) * s (dequant8, common.h): (q - z)
+// is exact in f16 and the product is rounded once (relative error <= 2^-11),
+// which keeps the group scale out of the f32 accumulators.
 
 // Direct global -> LDS loads (each lane's 16 or 4 bytes land at the
 // wave-uniform LDS address + lane * size), addressed as a wave-uniform base
@@ -501,9 +499,8 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
   // sA: the group's token rows in LDS, row m at sA + 256 m
   auto compute = [&](int g, const uint8_t* sA, const WGroup& w) {
     const uint32_t z = (w.z >> (((t.zbase + g) & 1) * 4)) & 0xfu;
-    const f16x2 s2 = as_h2(w.s * 0x00010001u);
-    const f16x2 ss2 = f16x2{s2.x, (_Float16)(s2.y * (_Float16)0.0625f)};
-    const f16x2 zz2 = as_h2((0x6400u | z) | ((0x6400u | (z << 4)) << 16));
+    const f16x2 ss2 = u4_ss2(w.s);
+    const f16x2 zz2 = u4_zz2(z);
     auto bfrag = [&](int mb, int j) {
       const int m = mb * 32 + n;
       const int slot = (hh * 8 + j) ^ (m & 15);
@@ -661,30 +658,41 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
   const int64_t H = L.hidden, I = L.inter;
   const int64_t K = GATEUP ? H : I;
   t.GK = (int)(K / 128);
-  const int64_t rows_e = GATEUP ? 2 * I : H;
 
-  const aima_u4_tensor& W = GATEUP ? (t.e < t.E ? L.gate_up : L.shared_gate_up)
-                                   : (t.e < t.E ? L.down : L.shared_down);
-  const int64_t eoff = (t.e < t.E) ? t.e : 0;
+  const bool routed_tile = t.e < t.E;
+  const int64_t eoff = routed_tile ? t.e : 0;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   // weight row (within the expert) of MFMA row i = lane % 32 of this wave
-  int64_t my_row;
+  // (gate/up: MFMA rows i / 8 = 0, 1 are gate rows, 2, 3 up rows of the same
+  // 16 intermediate units; either boundary form of the gate/up tensors)
+  int64_t wrow;
+  const uint8_t* wq;
+  const uint16_t* ws;
+  const uint8_t* wz;
   {
     const int i = lane & 31;
     if (GATEUP) {
+      const GateUpView V = routed_tile ? routed_gate_up(L) : shared_gate_up(L);
       const int q = i >> 3;
+      const int h = q >> 1;
       const int64_t j = (int64_t)t.ntile * 128 + wave * 16 + 8 * (q & 1) + (i & 7);
-      my_row = q < 2 ? j : I + j;
+      wrow = V.row(eoff, h, j);
+      wq = V.q[h];
+      ws = V.s[h];
+      wz = V.z[h];
     } else {
-      my_row = (int64_t)t.ntile * 256 + wave * 32 + i;
+      const aima_u4_tensor& W = routed_tile ? L.down : L.shared_down;
+      wrow = eoff * H + (int64_t)t.ntile * 256 + wave * 32 + i;
+      wq = W.qweight;
+      ws = W.scale;
+      wz = W.zp;
     }
   }
-  const int64_t wrow = eoff * rows_e + my_row;
-  t.wq = W.qweight + wrow * (K / 2) + (lane >> 5) * 32;
-  t.ws = W.scale + wrow * t.GK;
-  t.wz = W.zp;
+  t.wq = wq + wrow * (K / 2) + (lane >> 5) * 32;
+  t.ws = ws + wrow * t.GK;
+  t.wz = wz;
   t.zbase = wrow * t.GK;
 
   // Token-row loads: block instruction q covers rows 4 q .. 4 q + 3; lane ->
@@ -891,6 +899,44 @@ __global__ __launch_bounds__(256) void combine2048_kernel(
 }
 
 
+// RunLayer's output (grouped_s8_u4_prefill_runtime.hpp:100-121): the f32 routed
+// sum out[t][h] = sum over ranks r (in order, from 0) of the f16 contribution
+// rows, as the reference's iq36_scatter_f16_contributions
+// (grouped_s8_u4_f16_contribution_moe.cl:831-845).  One block per token.
+__global__ __launch_bounds__(256) void combine_routed_f32_kernel(
+    const uint16_t* __restrict__ contrib, const int32_t* __restrict__ inverse_map, int k,
+    int64_t H, float* __restrict__ out) {
+  __shared__ int rowsel[16];
+  const int64_t t = blockIdx.x;
+  if (threadIdx.x < k) rowsel[threadIdx.x] = inverse_map[t * k + threadIdx.x];
+  __syncthreads();
+  for (int64_t h = threadIdx.x * 8; h < H; h += 2048) {
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < k; ++r) {
+      const u32x4 c = *reinterpret_cast<const u32x4*>(contrib + (int64_t)rowsel[r] * H + h);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t wj = c[j];
+        s[2 * j] += h2f((uint16_t)(wj & 0xffffu));
+        s[2 * j + 1] += h2f((uint16_t)(wj >> 16));
+      }
+    }
+    float4* o = reinterpret_cast<float4*>(out + t * H + h);
+    o[0] = make_float4(s[0], s[1], s[2], s[3]);
+    o[1] = make_float4(s[4], s[5], s[6], s[7]);
+  }
+}
+
+// f32 hidden states (RunLayer's input type) -> f16 GEMM operands, round to
+// nearest even; 8 values per thread.
+__global__ __launch_bounds__(256) void f32_to_f16_kernel(const float4* __restrict__ in,
+                                                         int64_t n8, u32x4* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const float4 a = in[2 * i], b = in[2 * i + 1];
+  out[i] = u32x4{pack_h2(a.x, a.y), pack_h2(a.z, a.w), pack_h2(b.x, b.y), pack_h2(b.z, b.w)};
+}
+
 // ---------------------------------------------------------------------------
 // host
 // ---------------------------------------------------------------------------
@@ -900,33 +946,53 @@ static int expert_bits(int E) {
   return b;
 }
 
-static int launch_schedule(const int32_t* ids, const float* weights, const PrefillDims& d,
-                           const PrefillWs& w, hipStream_t st) {
+// stride: int32 words between two tokens' top-k rows; with_shared: emit the
+// shared expert's tiles (rows A .. A + T - 1).
+static int launch_schedule(const int32_t* ids, int stride, const float* weights,
+                           const PrefillDims& d, const PrefillWs& w, bool with_shared,
+                           hipStream_t st) {
   const int bits = expert_bits(d.E);
   int Ep = 1;
   while (Ep < d.E) Ep <<= 1;
   hipLaunchKernelGGL(sched_count_kernel, dim3((unsigned)d.nb), dim3(kSchedBlock), 0, st, ids,
-                     (int32_t)d.A, d.k, d.E, bits, w.err, w.block_base, w.inverse_map);
+                     stride, (int32_t)d.A, d.k, d.E, bits, w.err, w.block_base, w.inverse_map);
   int rc = launch_check("grouped schedule count");
   if (rc != AIMA_OK) return rc;
   hipLaunchKernelGGL(sched_scan_kernel, dim3(1), dim3(1024), 0, st, w.block_base, (int32_t)d.nb,
-                     d.E, Ep, (int32_t)d.T, (int32_t)d.A, w.offsets, w.tiles, w.tile_count);
+                     d.E, Ep, (int32_t)d.T, (int32_t)d.A, with_shared ? 1 : 0, w.offsets, w.tiles,
+                     w.tile_count);
   rc = launch_check("grouped schedule scan");
   if (rc != AIMA_OK) return rc;
   hipLaunchKernelGGL(sched_scatter_kernel, dim3((unsigned)d.nb), dim3(kSchedBlock), 0, st, ids,
-                     weights, (int32_t)d.A, d.k, d.E, w.block_base, w.token_map, w.inverse_map,
-                     w.row_weight);
+                     stride, weights, (int32_t)d.A, d.k, d.E, w.block_base, w.token_map,
+                     w.inverse_map, w.row_weight);
   return launch_check("grouped schedule scatter");
+}
+
+// How one layer call runs beyond the default (f16 in, routed + shared +
+// residual f16 out, dense top-k rows).
+struct LayerCall {
+  int stride = 0;               // int32 words between top-k rows (0: k)
+  bool routed_f32 = false;      // RunLayer output: f32 routed sum, no shared expert
+  hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+};
+
+static int record(hipEvent_t e, hipStream_t st) {
+  return e ? hip_check(hipEventRecord(e, st), "hipEventRecord(prefill stage)") : AIMA_OK;
 }
 
 // sigma_in: the shared-expert gate per token if already known (null: the
 // combine computes it from x); next: fusion of the next layer's input.
 static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint16_t* residual,
-                         const int32_t* ids, const float* weights, uint16_t* out,
+                         const int32_t* ids, const float* weights, void* out,
                          const PrefillDims& d, const PrefillWs& w, hipStream_t st,
-                         const float* sigma_in = nullptr, CombineNext next = CombineNext{}) {
-  int rc = launch_schedule(ids, weights, d, w, st);
+                         const float* sigma_in = nullptr, CombineNext next = CombineNext{},
+                         const LayerCall& call = LayerCall{}) {
+  int rc = record(call.ev[0], st);
   if (rc != AIMA_OK) return rc;
+  rc = launch_schedule(ids, call.stride ? call.stride : d.k, weights, d, w, !call.routed_f32, st);
+  if (rc != AIMA_OK) return rc;
+  if ((rc = record(call.ev[1], st)) != AIMA_OK) return rc;
   const unsigned mtiles = (unsigned)round_up(d.max_tiles, 8);
   {
     const int nt = d.I / 128;
@@ -936,6 +1002,7 @@ static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint1
   }
   rc = launch_check("grouped gate/up GEMM");
   if (rc != AIMA_OK) return rc;
+  if ((rc = record(call.ev[2], st)) != AIMA_OK) return rc;
   {
     const int nt = d.H / 256;
     hipLaunchKernelGGL((grouped_gemm_kernel<false>), dim3(mtiles * nt), dim3(kGemmThreads), 0, st,
@@ -944,16 +1011,22 @@ static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint1
   }
   rc = launch_check("grouped down GEMM");
   if (rc != AIMA_OK) return rc;
-  if (d.H == 2048 && d.k <= 8) {
+  if ((rc = record(call.ev[3], st)) != AIMA_OK) return rc;
+  if (call.routed_f32) {
+    hipLaunchKernelGGL(combine_routed_f32_kernel, dim3((unsigned)d.T), dim3(256), 0, st,
+                       w.contrib, w.inverse_map, d.k, (int64_t)d.H, static_cast<float*>(out));
+  } else if (d.H == 2048 && d.k <= 8) {
     hipLaunchKernelGGL(combine2048_kernel, dim3((unsigned)d.T), dim3(256), 0, st, w.contrib,
-                       w.inverse_map, d.k, d.A, x, L.shared_gate_vec, sigma_in, residual, out,
-                       next);
+                       w.inverse_map, d.k, d.A, x, L.shared_gate_vec, sigma_in, residual,
+                       static_cast<uint16_t*>(out), next);
   } else {
     hipLaunchKernelGGL(combine_kernel, dim3((unsigned)d.T), dim3(256), 0, st, w.contrib,
                        w.inverse_map, d.k, d.A, x, L.shared_gate_vec, sigma_in, residual,
-                       (int64_t)d.H, out, next);
+                       (int64_t)d.H, static_cast<uint16_t*>(out), next);
   }
-  return launch_check("grouped combine");
+  rc = launch_check("grouped combine");
+  if (rc != AIMA_OK) return rc;
+  return record(call.ev[4], st);
 }
 
 // The grouped GEMM addresses its A rows with 32-bit byte offsets.
@@ -962,27 +1035,37 @@ static bool prefill_offsets_fit(const aima_moe_layer* L, int64_t tokens, int k) 
   return tokens * (k + 1) * L->inter < limit && tokens * L->hidden < limit;
 }
 
-int check_layer_prefill(const aima_moe_layer* L, int k, bool need_norm) {
+// need_shared: the call runs the shared expert (every mode but the routed-only
+// RunLayer output, which needs no shared tensors).
+int check_layer_prefill(const aima_moe_layer* L, int k, bool need_norm, bool need_shared = true) {
   AIMA_REQUIRE(L != nullptr, "moe prefill: null layer");
   AIMA_REQUIRE(L->gate_up.qweight && L->gate_up.scale && L->gate_up.zp && L->down.qweight &&
-                   L->down.scale && L->down.zp && L->shared_gate_up.qweight &&
-                   L->shared_gate_up.scale && L->shared_gate_up.zp && L->shared_down.qweight &&
-                   L->shared_down.scale && L->shared_down.zp && L->shared_gate_vec,
-               "moe prefill: null tensor pointer");
+                   L->down.scale && L->down.zp,
+               "moe prefill: null routed tensor pointer");
+  AIMA_REQUIRE(!need_shared || (L->shared_gate_up.qweight && L->shared_gate_up.scale &&
+                                L->shared_gate_up.zp && L->shared_down.qweight &&
+                                L->shared_down.scale && L->shared_down.zp && L->shared_gate_vec),
+               "moe prefill: null shared tensor pointer");
+  AIMA_REQUIRE(split_tensors_ok(*L),
+               "moe prefill: a split up tensor needs qweight, scale and zp (qweight 16-byte aligned)");
   AIMA_REQUIRE(!need_norm || L->norm_weight, "moe prefill: null norm weight");
   AIMA_REQUIRE(L->experts > 0 && L->experts <= kMaxExperts, "moe prefill: experts must be in [1, 1024]");
   AIMA_REQUIRE(k > 0 && k <= 16 && k <= L->experts, "moe prefill: k must be in [1, min(16, experts)]");
   if (L->group != 128) return fail(AIMA_E_UNSUPPORTED, "moe prefill: group must be 128");
-  if (L->shared_inter != L->inter) {
+  if (need_shared && L->shared_inter != L->inter) {
     return fail(AIMA_E_UNSUPPORTED, "moe prefill: shared_inter must equal inter");
   }
   if (L->hidden % 256 != 0 || L->inter % 128 != 0 || L->hidden <= 0 || L->inter <= 0) {
     return fail(AIMA_E_UNSUPPORTED, "moe prefill: hidden % 256 and inter % 128 must be 0");
   }
   AIMA_REQUIRE(aligned(L->gate_up.qweight, 16) && aligned(L->down.qweight, 16) &&
-                   aligned(L->shared_gate_up.qweight, 16) && aligned(L->shared_down.qweight, 16) &&
-                   aligned(L->shared_gate_vec, 16),
+                   (!need_shared || (aligned(L->shared_gate_up.qweight, 16) &&
+                                     aligned(L->shared_down.qweight, 16) &&
+                                     aligned(L->shared_gate_vec, 16))),
                "moe prefill: qweight pointers and the shared gate vector must be 16-byte aligned");
+  // the stack's fused combine reads the next layer's norm weights as 16-byte vectors
+  AIMA_REQUIRE(!need_norm || aligned(L->norm_weight, 16),
+               "moe prefill: norm_weight must be 16-byte aligned");
   return AIMA_OK;
 }
 
@@ -1031,6 +1114,79 @@ extern "C" int aima_moe_grouped_prefill(const aima_moe_layer* layer, const uint1
   }
   AIMA_REQUIRE(aligned(workspace, 256), "moe_grouped_prefill: workspace must be 256-byte aligned");
   return prefill_layer(*layer, x, residual, ids, weights, out, d, w, (hipStream_t)stream);
+}
+
+extern "C" int aima_moe_grouped_prefill_ex(const aima_moe_layer* layer, const void* x,
+                                           const uint16_t* residual, int64_t tokens,
+                                           const int32_t* topk, const float* weights, int32_t k,
+                                           void* out, const aima_prefill_options* options,
+                                           void* workspace, size_t workspace_bytes,
+                                           void* stream) {
+  aima_prefill_options opt{};
+  if (options) opt = *options;
+  AIMA_REQUIRE(opt.output_mode == AIMA_PREFILL_FULL_F16 || opt.output_mode == AIMA_PREFILL_ROUTED_F32,
+               "moe_grouped_prefill_ex: unknown output mode");
+  AIMA_REQUIRE(opt.input_f32 == 0 || opt.input_f32 == 1, "moe_grouped_prefill_ex: input_f32 must be 0 or 1");
+  const bool routed = opt.output_mode == AIMA_PREFILL_ROUTED_F32;
+  int rc = check_layer_prefill(layer, k, false, !routed);
+  if (rc != AIMA_OK) return rc;
+  AIMA_REQUIRE(x && topk && weights && out, "moe_grouped_prefill_ex: null pointer");
+  AIMA_REQUIRE(!routed || !residual,
+               "moe_grouped_prefill_ex: the routed-only output takes no residual");
+  AIMA_REQUIRE(tokens > 0 && tokens <= (1 << 24), "moe_grouped_prefill_ex: tokens must be in [1, 2^24]");
+  // RunLayer requires topk_stride >= 8 * sizeof(int32) for its top-8
+  // (grouped_s8_u4_prefill_runtime.cpp:1044-1045); here >= k * 4
+  const int64_t stride_bytes = opt.topk_stride ? opt.topk_stride : (int64_t)k * 4;
+  AIMA_REQUIRE(stride_bytes >= (int64_t)k * 4 && stride_bytes % 4 == 0 &&
+                   stride_bytes / 4 <= (1 << 20),
+               "moe_grouped_prefill_ex: topk_stride must be a multiple of 4, >= 4 * k and <= 4 MiB");
+  AIMA_REQUIRE(aligned(topk, 4), "moe_grouped_prefill_ex: topk must be 4-byte aligned");
+  AIMA_REQUIRE(prefill_offsets_fit(layer, tokens, k),
+               "moe_grouped_prefill_ex: tokens * (k + 1) * inter and tokens * hidden must stay "
+               "below 2^30 (split the batch)");
+  AIMA_REQUIRE(aligned(x, 16) && aligned(out, 16) && (!residual || aligned(residual, 16)),
+               "moe_grouped_prefill_ex: x, residual and out must be 16-byte aligned");
+  const PrefillDims d = prefill_dims(layer, tokens, k);
+  PrefillWs w{};
+  const size_t need = prefill_ws_layout(d, WsMode::kLayer, workspace, &w);
+  if (!workspace || workspace_bytes < need) {
+    return fail(AIMA_E_WORKSPACE, "moe_grouped_prefill_ex: workspace missing or too small");
+  }
+  AIMA_REQUIRE(aligned(workspace, 256), "moe_grouped_prefill_ex: workspace must be 256-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  LayerCall call;
+  call.stride = (int)(stride_bytes / 4);
+  call.routed_f32 = routed;
+  for (int i = 0; i < 5; ++i) call.ev[i] = static_cast<hipEvent_t>(opt.stage_events[i]);
+  const uint16_t* x16 = static_cast<const uint16_t*>(x);
+  if (opt.input_f32) {
+    const int64_t n8 = tokens * layer->hidden / 8;
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, st,
+                       static_cast<const float4*>(x), n8, reinterpret_cast<u32x4*>(w.x16));
+    rc = launch_check("moe_grouped_prefill_ex input conversion");
+    if (rc != AIMA_OK) return rc;
+    x16 = w.x16;
+  }
+  return prefill_layer(*layer, x16, residual, topk, weights, out, d, w, st, nullptr,
+                       CombineNext{}, call);
+}
+
+extern "C" int aima_moe_prefill_workspace_views(const aima_moe_layer* layer, int64_t tokens,
+                                                int32_t k, void* workspace,
+                                                aima_prefill_views* views) {
+  AIMA_REQUIRE(layer && workspace && views, "moe_prefill_workspace_views: null pointer");
+  AIMA_REQUIRE(tokens > 0 && k > 0, "moe_prefill_workspace_views: tokens and k must be positive");
+  PrefillWs w{};
+  prefill_ws_layout(prefill_dims(layer, tokens, k), WsMode::kLayer, workspace, &w);
+  views->offsets = w.offsets;
+  views->token_map = w.token_map;
+  views->inverse_map = w.inverse_map;
+  views->compact_weights = w.row_weight;
+  views->weighted_swiglu = w.act;
+  views->contributions = w.contrib;
+  views->tiles = w.tiles;
+  views->tile_count = w.tile_count;
+  return AIMA_OK;
 }
 
 extern "C" int aima_moe_stack_prefill(const aima_moe_layer* layers, int32_t n_layers, float eps,
@@ -1109,7 +1265,7 @@ extern "C" int aima_grouped_schedule(const int32_t* ids, const float* weights, i
   }
   AIMA_REQUIRE(aligned(workspace, 256), "grouped_schedule: workspace must be 256-byte aligned");
   hipStream_t st = (hipStream_t)stream;
-  int rc = launch_schedule(ids, weights, d, w, st);
+  int rc = launch_schedule(ids, k, weights, d, w, true, st);
   if (rc != AIMA_OK) return rc;
   AIMA_HIP(hipMemcpyAsync(offsets, w.offsets, (size_t)experts * 4, hipMemcpyDeviceToDevice, st));
   AIMA_HIP(hipMemcpyAsync(token_map, w.token_map, (size_t)d.A * 4, hipMemcpyDeviceToDevice, st));

@@ -39,6 +39,23 @@ __global__ __launch_bounds__(256) void u4_dequant_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// f16 dequant: out[n][k] = f16(f32(q - z) * f32(s)), one thread per 8 codes,
+// through dequant8 -- the operand the grouped GEMM feeds its MFMAs
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void u4_dequant_f16_kernel(
+    const uint32_t* __restrict__ qw, const uint16_t* __restrict__ scale,
+    const uint8_t* __restrict__ zp, int64_t words, int64_t k, int group,
+    f16x8* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= words) return;
+  const int64_t words_per_row = k / 8;
+  const int64_t row = i / words_per_row;
+  const int64_t k0 = (i % words_per_row) * 8;
+  const int64_t gi = row * (k / group) + k0 / group;
+  out[i] = dequant8(qw[i], u4_zz2(u4_code(zp, gi)), u4_ss2(scale[gi]), u4_magic());
+}
+
+// ---------------------------------------------------------------------------
 // matvec
 // ---------------------------------------------------------------------------
 template <int KCH>
@@ -402,6 +419,22 @@ extern "C" int aima_u4_dequant(const uint8_t* qweight, const uint16_t* scale,
                      (hipStream_t)stream, reinterpret_cast<const uint32_t*>(qweight),
                      scale, zp, words, k, (int)group, reinterpret_cast<float4*>(out));
   return launch_check("u4_dequant");
+}
+
+extern "C" int aima_u4_dequant_f16(const uint8_t* qweight, const uint16_t* scale,
+                                   const uint8_t* zp, int64_t n, int64_t k, int32_t group,
+                                   uint16_t* out, void* stream) {
+  AIMA_REQUIRE(qweight && scale && zp && out, "u4_dequant_f16: null pointer");
+  AIMA_REQUIRE(n > 0 && k > 0, "u4_dequant_f16: n and k must be positive");
+  AIMA_REQUIRE(group > 0 && group % 32 == 0 && k % group == 0,
+               "u4_dequant_f16: group must be a multiple of 32 dividing k");
+  AIMA_REQUIRE(aligned(qweight, 4) && aligned(out, 16), "u4_dequant_f16: misaligned pointer");
+  const int64_t words = n * k / 8;
+  const int64_t blocks = (words + 255) / 256;
+  hipLaunchKernelGGL(u4_dequant_f16_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<const uint32_t*>(qweight),
+                     scale, zp, words, k, (int)group, reinterpret_cast<f16x8*>(out));
+  return launch_check("u4_dequant_f16");
 }
 
 extern "C" int aima_u4_matvec(const uint16_t* x, const uint8_t* qweight,

@@ -78,22 +78,37 @@ class U4Weight:
 
 @dataclass
 class MoeLayerWeights:
-    """One MoE FFN layer: routed expert stacks, the shared expert, its gate."""
+    """One MoE FFN layer: routed expert stacks, the shared expert, its gate.
 
-    gate_up: U4Weight                  # E x [2I][H]
+    Gate and up come in either boundary form: concatenated (``gate_up`` =
+    E x [2I][H], gate rows first; ``up`` is None) or split, the operands of
+    OpenVINO's MOE3GemmFusedCompressed (``gate_up`` = the gate projection
+    E x [I][H] and ``up`` = E x [I][H]; likewise ``shared_up``).
+    """
+
+    gate_up: U4Weight                  # E x [2I][H], or the gate E x [I][H] when split
     down: U4Weight                     # E x [H][I]
-    shared_gate_up: U4Weight           # [2I][H]
+    shared_gate_up: U4Weight           # [2I][H], or the shared gate [I][H] when split
     shared_down: U4Weight              # [H][I]
     shared_gate_vec: torch.Tensor      # float16 [H]
     norm_weight: Optional[torch.Tensor] = None  # float32 [H] (RMSNorm before the layer)
+    up: Optional[U4Weight] = None      # E x [I][H] (split form)
+    shared_up: Optional[U4Weight] = None  # [I][H] (split form)
 
     def __post_init__(self):
         H, I = self.hidden, self.inter
-        if self.gate_up.rows != 2 * I or self.down.rows != H or self.down.k != I:
+        if (self.up is None) != (self.shared_up is None):
+            raise ValueError("split form needs both up and shared_up")
+        if self.up is not None:
+            if (self.up.rows != self.gate_up.rows or self.up.k != H or
+                    self.up.experts != self.gate_up.experts or self.up.group != self.group or
+                    self.shared_up.rows != self.shared_gate_up.rows or self.shared_up.k != H):
+                raise ValueError("split up tensors must match the gate tensors")
+        if self.down.rows != H or self.down.k != I:
             raise ValueError("routed expert shapes disagree")
         if self.shared_gate_up.k != H or self.shared_down.rows != H:
             raise ValueError("shared expert shapes disagree")
-        if self.shared_down.k != self.shared_gate_up.rows // 2:
+        if self.shared_down.k != self.shared_inter:
             raise ValueError("shared down K must equal shared intermediate")
         if self.gate_up.experts != self.down.experts:
             raise ValueError("gate/up and down expert counts differ")
@@ -108,12 +123,16 @@ class MoeLayerWeights:
         return self.gate_up.k
 
     @property
+    def split(self) -> bool:
+        return self.up is not None
+
+    @property
     def inter(self) -> int:
-        return self.gate_up.rows // 2
+        return self.gate_up.rows if self.split else self.gate_up.rows // 2
 
     @property
     def shared_inter(self) -> int:
-        return self.shared_gate_up.rows // 2
+        return self.shared_gate_up.rows if self.split else self.shared_gate_up.rows // 2
 
     @property
     def experts(self) -> int:
@@ -125,13 +144,48 @@ class MoeLayerWeights:
 
     def expert_bytes(self) -> int:
         """Weight bytes of one routed expert (gate/up + down)."""
-        return self.gate_up.expert_bytes() + self.down.expert_bytes()
+        up = self.up.expert_bytes() if self.split else 0
+        return self.gate_up.expert_bytes() + up + self.down.expert_bytes()
 
     def shared_bytes(self) -> int:
-        return self.shared_gate_up.nbytes + self.shared_down.nbytes
+        up = self.shared_up.nbytes if self.split else 0
+        return self.shared_gate_up.nbytes + up + self.shared_down.nbytes
 
     def c(self) -> MoeLayerC:
+        none = U4TensorC(None, None, None)
         return MoeLayerC(self.gate_up.c(), self.down.c(), self.shared_gate_up.c(),
                          self.shared_down.c(), self.shared_gate_vec.data_ptr(),
                          self.norm_weight.data_ptr() if self.norm_weight is not None else None,
-                         self.hidden, self.inter, self.shared_inter, self.experts, self.group)
+                         self.hidden, self.inter, self.shared_inter, self.experts, self.group,
+                         self.up.c() if self.split else none,
+                         self.shared_up.c() if self.split else none)
+
+    def to_split(self) -> "MoeLayerWeights":
+        """The same layer in the split form (copies of the gate and up rows)."""
+        if self.split:
+            return self
+        gate, up = _split_rows(self.gate_up, self.inter)
+        sgate, sup = _split_rows(self.shared_gate_up, self.shared_inter)
+        return MoeLayerWeights(gate, self.down, sgate, self.shared_down, self.shared_gate_vec,
+                               self.norm_weight, up, sup)
+
+
+def _split_rows(w: U4Weight, inter: int):
+    """Concatenated [E][2I][K] -> (gate [E][I][K], up [E][I][K]) U4 tensors."""
+    e, G = w.experts, w.groups
+    q = w.qweight.reshape(e, 2 * inter, w.k // 2)
+    s = w.scale.reshape(e, 2 * inter, G)
+    # zero points: nibbles over the flat [rows * G] index of each expert
+    zb = w.zp.reshape(e, -1)
+    nib = torch.stack([zb & 0xF, zb >> 4], dim=-1).reshape(e, 2 * inter, G)
+    out = []
+    for h in range(2):
+        n = nib[:, h * inter:(h + 1) * inter].reshape(e, -1)
+        zp = (n[:, 0::2] | (n[:, 1::2] << 4)).to(torch.uint8)
+        qq = q[:, h * inter:(h + 1) * inter].contiguous()
+        ss = s[:, h * inter:(h + 1) * inter].contiguous()
+        if w.qweight.dim() == 2:
+            qq, ss, zp = qq[0], ss[0], zp[0]
+        out.append(U4Weight(qq.contiguous(), ss.contiguous(), zp.contiguous(), inter, w.k,
+                            w.group))
+    return out

@@ -104,6 +104,17 @@ def u4_dequant(w: U4Weight) -> torch.Tensor:
     return out
 
 
+def u4_dequant_f16(w: U4Weight) -> torch.Tensor:
+    """f16(f32(q - z) * f32(s)) -> float16 [experts*rows, k]: the weight
+    operand the grouped prefill GEMM feeds its MFMAs, by the same routine."""
+    _require_cuda(w.qweight)
+    n = w.experts * w.rows
+    out = torch.empty((n, w.k), dtype=torch.float16, device=w.qweight.device)
+    call("aima_u4_dequant_f16", w.qweight.data_ptr(), w.scale.data_ptr(), w.zp.data_ptr(), n,
+         w.k, w.group, out.data_ptr(), _stream())
+    return out
+
+
 def matvec_u4(x: torch.Tensor, w: U4Weight, out_dtype=torch.float16) -> torch.Tensor:
     """y = W x for a batch-1 float16 activation x [k]; f32 accumulate."""
     _require_cuda(x, w.qweight)
@@ -375,6 +386,102 @@ def grouped_moe_prefill(layer: MoeLayerWeights, x: torch.Tensor, ids: torch.Tens
     return out
 
 
+def grouped_moe_prefill_routed(layer: MoeLayerWeights, hidden_states: torch.Tensor,
+                               topk: torch.Tensor, router_weights: torch.Tensor,
+                               topk_stride: Optional[int] = None, expert_used_count: int = 8,
+                               ws: Optional[Workspace] = None, stage_events=None) -> torch.Tensor:
+    """GroupedS8U4PrefillRuntime::RunLayer's operation: the f32 routed sum
+    out[t] = sum_r w[t][r] * down_r(swiglu(gate_up_r x_t)) (no shared expert,
+    no residual).
+
+    hidden_states: float32 or float16 [T, H]; topk: int32 ids with token t's
+    ``expert_used_count`` ids at byte offset t * topk_stride (a 2-D [T, >= k]
+    tensor uses its row stride; a flat int32 or uint8 buffer needs
+    ``topk_stride``); router_weights: float32 [T * k] (or [T, k]).
+    stage_events: optional five torch.cuda.Event recorded around the stages.
+    """
+    _require_cuda(hidden_states, topk, router_weights)
+    if hidden_states.dtype not in (torch.float32, torch.float16) or hidden_states.dim() != 2 \
+            or hidden_states.shape[1] != layer.hidden:
+        raise ValueError("hidden_states must be float32 or float16 [tokens, hidden]")
+    x = hidden_states.contiguous()
+    T = x.shape[0]
+    k = int(expert_used_count)
+    if topk.dtype == torch.uint8:
+        if topk_stride is None:
+            raise ValueError("a byte top-k buffer needs topk_stride")
+        stride = int(topk_stride)
+    elif topk.dtype == torch.int32:
+        if topk.dim() == 2:
+            if topk.stride(1) != 1 or topk.shape[1] < k:
+                raise ValueError("top-k rows must be contiguous with at least k ids")
+            stride = int(topk_stride) if topk_stride is not None else topk.stride(0) * 4
+        else:
+            stride = int(topk_stride) if topk_stride is not None else k * 4
+    else:
+        raise TypeError("topk must be int32 (or uint8 bytes)")
+    if stride < 4 * k or stride % 4:
+        raise ValueError("topk_stride must be a multiple of 4 and at least 4 * k bytes")
+    # the reference's check: (T - 1) * stride + k ids must lie inside the payload
+    # (grouped_s8_u4_prefill_runtime.cpp:234-236)
+    need = (T - 1) * stride + k * 4
+    avail = topk.untyped_storage().nbytes() - topk.storage_offset() * topk.element_size()
+    if avail < need:
+        raise ValueError("top-k payload is truncated")
+    if router_weights.dtype != torch.float32 or router_weights.numel() != T * k:
+        raise ValueError("router_weights must be float32 with tokens * k values")
+    rw = router_weights.contiguous()
+    lc = layer.c()
+    ws = _ws(ws, x.device)
+    buf = ws.get(size_query("aima_moe_prefill_workspace_size", C.byref(lc), T, k))
+    out = torch.empty((T, layer.hidden), dtype=torch.float32, device=x.device)
+    opt = _lib.PrefillOptionsC()
+    opt.output_mode = _lib.AIMA_PREFILL_ROUTED_F32
+    opt.input_f32 = 1 if x.dtype == torch.float32 else 0
+    opt.topk_stride = stride
+    if stage_events is not None:
+        if len(stage_events) != 5:
+            raise ValueError("five stage events")
+        for i, e in enumerate(stage_events):
+            if e is not None and not e.cuda_event:
+                e.record(torch.cuda.current_stream())  # torch creates its events lazily
+            opt.stage_events[i] = e.cuda_event if e is not None else None
+    call("aima_moe_grouped_prefill_ex", C.byref(lc), x.data_ptr(), None, T, topk.data_ptr(),
+         rw.data_ptr(), k, out.data_ptr(), C.byref(opt), buf.data_ptr(), buf.numel(), _stream())
+    return out
+
+
+def prefill_workspace_views(layer: MoeLayerWeights, tokens: int, k: int, ws: Workspace,
+                            with_shared: bool = True) -> dict:
+    """Tensor views of the intermediates the last prefill call left in ``ws``
+    (schedule, router-weighted SwiGLU rows and down contributions, in
+    schedule order; aliases of the workspace, valid until its next use)."""
+    if ws.buf is None:
+        raise ValueError("workspace was never used")
+    lc = layer.c()
+    v = _lib.PrefillViewsC()
+    call("aima_moe_prefill_workspace_views", C.byref(lc), int(tokens), int(k), ws.buf.data_ptr(),
+         C.byref(v))
+    base = ws.buf.data_ptr()
+    A = tokens * k
+    rows = A + (tokens if with_shared else 0)
+
+    def view(ptr, n, dtype):
+        off = ptr - base
+        esz = torch.tensor([], dtype=dtype).element_size()
+        return ws.buf[off:off + n * esz].view(dtype)
+
+    return {"offsets": view(v.offsets, layer.experts, torch.int32),
+            "token_map": view(v.token_map, A, torch.int32),
+            "inverse_map": view(v.inverse_map, A, torch.int32),
+            "compact_weights": view(v.compact_weights, A, torch.float32),
+            "weighted_swiglu": view(v.weighted_swiglu, rows * layer.inter,
+                                    torch.float16).reshape(rows, layer.inter),
+            "contributions": view(v.contributions, rows * layer.hidden,
+                                  torch.float16).reshape(rows, layer.hidden),
+            "tile_count": view(v.tile_count, 1, torch.int32)}
+
+
 def build_grouped_schedule(ids: torch.Tensor, router_weights: torch.Tensor, experts: int,
                            ws: Optional[Workspace] = None) -> dict:
     """Device BuildGroupedSchedule: offsets [E], token_map/inverse_map/compact_weights [T*k]."""
@@ -494,6 +601,9 @@ class DecodePlan:
     select_router_topk rule) or from ``ids``/``weights`` [L, k].
     Raises AimaError(AIMA_E_UNSUPPORTED) for shapes outside the specialization
     (hidden 2048, inter 512, k <= 8); ``moe_stack_decode`` covers those.
+    ``run`` is asynchronous: its output is valid only if ``check()`` (or
+    ``error_bits()``) afterwards reports no device error -- a wait that hit
+    its spin limit leaves ``out`` unwritten.
     """
 
     def __init__(self, layers: Sequence[MoeLayerWeights], k: int = 8):
@@ -511,10 +621,11 @@ class DecodePlan:
             out: Optional[torch.Tensor] = None) -> torch.Tensor:
         if self._h is None:
             raise RuntimeError("decode plan was closed")
-        _require_cuda(residual, router_logits, ids, weights)
+        _require_cuda(residual, router_logits, ids, weights, out)
         L = len(self.layers)
-        if residual.dtype != torch.float16 or residual.numel() != self.hidden:
-            raise ValueError("residual must be float16 [hidden]")
+        if residual.dtype != torch.float16 or residual.numel() != self.hidden or \
+                not residual.is_contiguous() or residual.data_ptr() % 16:
+            raise ValueError("residual must be a contiguous, 16-byte aligned float16 [hidden]")
         if router_logits is not None:
             if router_logits.dtype != torch.float32 or router_logits.dim() != 2 or \
                     router_logits.shape[0] != L or not router_logits.is_contiguous():
@@ -528,6 +639,8 @@ class DecodePlan:
                 raise ValueError("ids/weights must be [layers, k]")
         if out is None:
             out = torch.empty(self.hidden, dtype=torch.float16, device=residual.device)
+        elif out.dtype != torch.float16 or out.numel() != self.hidden or not out.is_contiguous():
+            raise ValueError("out must be a contiguous float16 [hidden]")
         call("aima_moe_decode_plan_run", self._h, float(epsilon), residual.data_ptr(),
              _ptr(router_logits), _ptr(ids), _ptr(weights), float(min_weight_sum),
              out.data_ptr(), _stream())

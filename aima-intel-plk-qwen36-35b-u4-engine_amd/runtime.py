@@ -1,14 +1,22 @@
 """Resident grouped-prefill runtime with the reference runtime's contract.
 
 Mirrors ``iq36::GroupedS8U4PrefillRuntime``
-(engine/include/intel_qwen36/grouped_s8_u4_prefill_runtime.hpp:137-162):
+(engine/include/intel_qwen36/grouped_s8_u4_prefill_runtime.hpp:62-162):
 ``LoadLayer`` makes a layer resident and returns a handle, ``RunLayer`` runs
 warmup + timed repeats of the complete grouped layer and returns the output
-with min/median/mean timings (grouped_s8_u4_prefill_runtime.cpp:1375-1432).
+with min/median/mean timings and per-stage times
+(grouped_s8_u4_prefill_runtime.cpp:1375-1432).
+
 The input record keeps the reference field names (hidden_states, topk,
-router_weights, warmup, repeat, capture_intermediates).  Differences: the
-weights are already U4 tensors on the device (no prep directory), inputs are
-device tensors, and timing uses HIP events on the current stream.
+topk_stride, router_weights, warmup, repeat, capture_intermediates) and the
+output is RunLayer's: the f32 routed sum ``sum_r w_r * down_r(...)`` per
+token.  ``include_shared=True`` (an extension) returns instead the complete
+f16 block output with the sigmoid-gated shared expert and an optional
+residual.  Differences: the weights are already U4 tensors on the device (no
+prep directory), inputs are device tensors, the schedule is always built on
+the device (the reference's ``device_schedule``), and timing uses HIP events
+on the current stream.  Intermediates come from the last timed repeat's own
+workspace, not from a second run.
 """
 
 from __future__ import annotations
@@ -22,20 +30,27 @@ import torch
 from . import ops
 from .layout import MoeLayerWeights
 
+# stage_us[i]: schedule, gate/up GEMM + SwiGLU, down GEMM, combine
+STAGES = ("schedule", "gate_up", "down", "combine")
+
 
 @dataclass
 class GroupedU4PrefillInput:
-    hidden_states: torch.Tensor          # float16 [T, H]
-    topk: torch.Tensor                   # int32 [T, k]
-    router_weights: torch.Tensor         # float32 [T, k]
-    residual: Optional[torch.Tensor] = None
+    hidden_states: torch.Tensor          # float32 or float16 [T, H]
+    topk: torch.Tensor                   # int32 ids [T, >= k] (or bytes, with topk_stride)
+    router_weights: torch.Tensor         # float32 [T * k] (or [T, k])
+    topk_stride: int = 0                 # bytes between tokens' id rows (0: from topk)
+    expert_used_count: int = 8
     warmup: int = 0
     repeat: int = 1
     capture_intermediates: bool = False
+    include_shared: bool = False         # extension: f16 routed + shared (+ residual)
+    residual: Optional[torch.Tensor] = None
 
 
 @dataclass
 class GroupedU4PrefillTiming:
+    stage_us: List[float] = field(default_factory=lambda: [0.0] * len(STAGES))
     samples_us: List[float] = field(default_factory=list)
     minimum_us: float = 0.0
     median_us: float = 0.0
@@ -45,11 +60,17 @@ class GroupedU4PrefillTiming:
 @dataclass
 class GroupedU4PrefillRun:
     output: torch.Tensor
+    # intermediates (capture_intermediates), in schedule order:
+    grouped_weighted_swiglu_f16: Optional[torch.Tensor] = None  # w_r * silu(g) * u, [rows][I]
+    grouped_contributions_f16: Optional[torch.Tensor] = None    # w_r * down, [rows][H]
     inverse_map: Optional[torch.Tensor] = None
     token_map: Optional[torch.Tensor] = None
     offsets: Optional[torch.Tensor] = None
     active_experts: int = 0
     max_group_size: int = 0
+    gateup_work_tile_count: int = 0
+    device_schedule: bool = True
+    native_router: bool = False
     timing: GroupedU4PrefillTiming = field(default_factory=GroupedU4PrefillTiming)
 
 
@@ -60,7 +81,7 @@ class GroupedU4PrefillRuntime:
         self._next = 1
         self._ws = ops.Workspace(self.device)
         self._stats = {"layer_load_count": 0, "layer_count": 0, "run_count": 0,
-                       "resident_weight_bytes": 0}
+                       "resident_weight_bytes": 0, "device_schedule_run_count": 0}
 
     def LoadLayer(self, weights: MoeLayerWeights) -> int:
         if weights.gate_up.qweight.device.type != "cuda":
@@ -71,6 +92,7 @@ class GroupedU4PrefillRuntime:
         self._stats["layer_load_count"] += 1
         self._stats["layer_count"] = len(self._layers)
         self._stats["resident_weight_bytes"] += (weights.gate_up.nbytes + weights.down.nbytes +
+                                                 (weights.up.nbytes if weights.split else 0) +
                                                  weights.shared_bytes())
         return handle
 
@@ -83,42 +105,69 @@ class GroupedU4PrefillRuntime:
         layer = self._layer(handle)
         if inp.warmup < 0 or inp.repeat <= 0:
             raise ValueError("grouped prefill warmup/repeat are invalid")
-        T = inp.hidden_states.shape[0]
-        if inp.topk.shape[0] != T or inp.router_weights.shape != inp.topk.shape:
-            raise ValueError("grouped prefill top-k / router weight shape mismatch")
+        x = inp.hidden_states
+        if x.dim() != 2 or x.shape[1] != layer.hidden:
+            raise ValueError("grouped prefill hidden-state count mismatch")
+        T, k = x.shape[0], int(inp.expert_used_count)
+        if inp.router_weights.numel() != T * k:
+            raise ValueError("grouped prefill router weight count mismatch")
+        stride = inp.topk_stride or None
+        if inp.include_shared:
+            if inp.topk.dtype != torch.int32 or inp.topk.shape != (T, k) or stride:
+                raise ValueError("include_shared takes dense int32 top-k [T, k]")
+            if x.dtype != torch.float16:
+                raise ValueError("include_shared takes float16 hidden states")
 
-        def execute():
-            return ops.grouped_moe_prefill(layer, inp.hidden_states, inp.topk, inp.router_weights,
-                                           residual=inp.residual, ws=self._ws)
+        stage_events = [torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)]
+
+        def execute(events=None):
+            if inp.include_shared:
+                return ops.grouped_moe_prefill(layer, x, inp.topk,
+                                               inp.router_weights.reshape(T, k),
+                                               residual=inp.residual, ws=self._ws)
+            return ops.grouped_moe_prefill_routed(layer, x, inp.topk, inp.router_weights,
+                                                  topk_stride=stride, expert_used_count=k,
+                                                  ws=self._ws, stage_events=events)
 
         for _ in range(inp.warmup):
             execute()
         stream = torch.cuda.current_stream()
-        samples = []
+        samples, stages = [], []
         out = None
         for _ in range(inp.repeat):
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
             start.record(stream)
-            out = execute()
+            out = execute(None if inp.include_shared else stage_events)
             end.record(stream)
             end.synchronize()
             samples.append(start.elapsed_time(end) * 1000.0)
+            if not inp.include_shared:
+                stages.append([stage_events[i].elapsed_time(stage_events[i + 1]) * 1000.0
+                               for i in range(len(STAGES))])
         self._ws.check()
         srt = sorted(samples)
-        run = GroupedU4PrefillRun(output=out, timing=GroupedU4PrefillTiming(
-            samples_us=samples, minimum_us=srt[0], median_us=srt[len(srt) // 2],
-            mean_us=statistics.fmean(samples)))
+        timing = GroupedU4PrefillTiming(samples_us=samples, minimum_us=srt[0],
+                                        median_us=srt[len(srt) // 2],
+                                        mean_us=statistics.fmean(samples))
+        if stages:
+            timing.stage_us = [statistics.median(s[i] for s in stages) for i in range(len(STAGES))]
+        run = GroupedU4PrefillRun(output=out, timing=timing)
         if inp.capture_intermediates:
-            sched = ops.build_grouped_schedule(inp.topk, inp.router_weights, layer.experts)
-            counts = torch.diff(sched["offsets"], prepend=torch.zeros(1, dtype=torch.int32,
-                                                                      device=self.device))
-            run.inverse_map = sched["inverse_map"]
-            run.token_map = sched["token_map"]
-            run.offsets = sched["offsets"]
+            # the last repeat's schedule and intermediates, still in the workspace
+            v = ops.prefill_workspace_views(layer, T, k, self._ws, with_shared=inp.include_shared)
+            counts = torch.diff(v["offsets"], prepend=torch.zeros(1, dtype=torch.int32,
+                                                                  device=self.device))
+            run.inverse_map = v["inverse_map"].clone()
+            run.token_map = v["token_map"].clone()
+            run.offsets = v["offsets"].clone()
+            run.grouped_weighted_swiglu_f16 = v["weighted_swiglu"].clone()
+            run.grouped_contributions_f16 = v["contributions"].clone()
+            run.gateup_work_tile_count = int(v["tile_count"].item()) * (layer.inter // 128)
             run.active_experts = int((counts > 0).sum().item())
             run.max_group_size = int(counts.max().item())
         self._stats["run_count"] += 1
+        self._stats["device_schedule_run_count"] += 1
         return run
 
     def stats(self) -> dict:
@@ -128,4 +177,6 @@ class GroupedU4PrefillRuntime:
 def _to_device(w: MoeLayerWeights, device) -> MoeLayerWeights:
     return MoeLayerWeights(w.gate_up.to(device), w.down.to(device), w.shared_gate_up.to(device),
                            w.shared_down.to(device), w.shared_gate_vec.to(device),
-                           None if w.norm_weight is None else w.norm_weight.to(device))
+                           None if w.norm_weight is None else w.norm_weight.to(device),
+                           None if w.up is None else w.up.to(device),
+                           None if w.shared_up is None else w.shared_up.to(device))

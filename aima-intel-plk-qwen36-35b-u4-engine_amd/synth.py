@@ -6,6 +6,9 @@ scale s = f16(|N(0, 0.02)| + 1e-3), activations f16(N(0, 1)), router logits
 f32 N(0, 1), optional Zipf(s) expert popularity bias b_e = ln p_e with
 p_e ~ rank_e^-s over a seeded permutation of ranks, RMSNorm weight
 1 + N(0, 0.01), shared-expert gate vector f16(N(0, 1) / sqrt(hidden)).
+``scale_log2=(lo, hi)`` draws the scales log-uniformly from [2^lo, 2^hi]
+instead (parity cases for small scales: below 2^-14 they are f16
+subnormals).
 Works on any torch device; generation on the GPU is used for the large
 configurations (the 40-layer stack is ~17 GB of U4 weights).
 """
@@ -26,21 +29,27 @@ def generator(seed: int, device) -> torch.Generator:
 
 
 def u4_weight(experts: int, rows: int, k: int, group: int, gen: torch.Generator,
-              device) -> U4Weight:
+              device, scale_log2=None) -> U4Weight:
     G = k // group
     shape = (experts, rows, k // 2) if experts > 1 else (rows, k // 2)
     qweight = torch.randint(0, 256, shape, dtype=torch.uint8, generator=gen, device=device)
     zshape = (experts, (rows * G + 1) // 2) if experts > 1 else ((rows * G + 1) // 2,)
     zp = torch.randint(0, 256, zshape, dtype=torch.uint8, generator=gen, device=device)
     sshape = (experts, rows, G) if experts > 1 else (rows, G)
-    scale = (torch.randn(sshape, generator=gen, device=device) * 0.02).abs_().add_(1e-3)
+    if scale_log2 is None:
+        scale = (torch.randn(sshape, generator=gen, device=device) * 0.02).abs_().add_(1e-3)
+    else:
+        lo, hi = scale_log2
+        u = torch.rand(sshape, generator=gen, device=device)
+        scale = torch.exp2(lo + (hi - lo) * u)
     return U4Weight(qweight, scale.to(torch.float16), zp, rows, k, group)
 
 
-def u4_expert_stack(experts: int, rows: int, k: int, group: int, gen, device) -> U4Weight:
+def u4_expert_stack(experts: int, rows: int, k: int, group: int, gen, device,
+                    scale_log2=None) -> U4Weight:
     """Like u4_weight but always with a leading expert dimension."""
-    w = u4_weight(max(experts, 2), rows, k, group, gen, device) if experts == 1 else \
-        u4_weight(experts, rows, k, group, gen, device)
+    w = u4_weight(max(experts, 2), rows, k, group, gen, device, scale_log2) if experts == 1 \
+        else u4_weight(experts, rows, k, group, gen, device, scale_log2)
     if experts == 1:
         w = U4Weight(w.qweight[:1].contiguous(), w.scale[:1].contiguous(), w.zp[:1].contiguous(),
                      rows, k, group)
@@ -49,20 +58,23 @@ def u4_expert_stack(experts: int, rows: int, k: int, group: int, gen, device) ->
 
 def moe_layer(hidden: int = 2048, inter: int = 512, experts: int = 256, group: int = 128,
               seed: int = 0, device="cuda", shared_inter: int = None,
-              with_norm: bool = True) -> MoeLayerWeights:
+              with_norm: bool = True, scale_log2=None, split: bool = False) -> MoeLayerWeights:
+    """A seeded layer; ``split`` returns the same weights in the split
+    gate / up form (MOE3GemmFusedCompressed's operands)."""
     device = torch.device(device)
     gen = generator(seed, device)
     si = inter if shared_inter is None else shared_inter
-    gate_up = u4_expert_stack(experts, 2 * inter, hidden, group, gen, device)
-    down = u4_expert_stack(experts, hidden, inter, group, gen, device)
-    sgu = u4_weight(1, 2 * si, hidden, group, gen, device)
-    sd = u4_weight(1, hidden, si, group, gen, device)
+    gate_up = u4_expert_stack(experts, 2 * inter, hidden, group, gen, device, scale_log2)
+    down = u4_expert_stack(experts, hidden, inter, group, gen, device, scale_log2)
+    sgu = u4_weight(1, 2 * si, hidden, group, gen, device, scale_log2)
+    sd = u4_weight(1, hidden, si, group, gen, device, scale_log2)
     gate_vec = (torch.randn(hidden, generator=gen, device=device) /
                 math.sqrt(hidden)).to(torch.float16)
     norm = None
     if with_norm:
         norm = 1.0 + 0.01 * torch.randn(hidden, generator=gen, device=device)
-    return MoeLayerWeights(gate_up, down, sgu, sd, gate_vec, norm)
+    layer = MoeLayerWeights(gate_up, down, sgu, sd, gate_vec, norm)
+    return layer.to_split() if split else layer
 
 
 def activations(tokens: int, hidden: int, seed: int, device="cuda") -> torch.Tensor:

@@ -62,14 +62,23 @@ typedef struct aima_u4_tensor {
 } aima_u4_tensor;
 
 /* One MoE FFN layer, all device pointers.
- *   gate_up        E x [2*inter][hidden]
+ *   gate_up        E x [2*inter][hidden]  (rows 0..inter-1 gate, then up)
  *   down           E x [hidden][inter]
  *   shared_gate_up 1 x [2*shared_inter][hidden]
  *   shared_down    1 x [hidden][shared_inter]
  *   shared_gate_vec f16[hidden]; the shared expert is scaled by
  *                   sigmoid(dot(shared_gate_vec, h))
  *   norm_weight    f32[hidden] RMSNorm weight applied before the layer by the
- *                   stack entry points (may be NULL for single-layer calls). */
+ *                   stack entry points (may be NULL for single-layer calls).
+ *   up, shared_up  optional separate up projections, the operand form of the
+ *                   OpenVINO op MOE3GemmFusedCompressed(hidden, routing_logits,
+ *                   gate_w, gate_scale, gate_zp, up_w, up_scale, up_zp, down_*)
+ *                   (engine/openvino/iq36-fixed-fc-moe-router-compat.patch:49-56):
+ *                   when up.qweight is non-NULL, gate_up holds ONLY the gate
+ *                   rows, E x [inter][hidden], and up the up rows,
+ *                   E x [inter][hidden] (likewise shared_up / shared_gate_up
+ *                   with 1 x [shared_inter][hidden]).  All-NULL (zeroed) = the
+ *                   concatenated form.  No entry point repacks either form. */
 typedef struct aima_moe_layer {
   aima_u4_tensor gate_up;
   aima_u4_tensor down;
@@ -82,12 +91,15 @@ typedef struct aima_moe_layer {
   int32_t shared_inter;
   int32_t experts;
   int32_t group;
+  aima_u4_tensor up;
+  aima_u4_tensor shared_up;
 } aima_moe_layer;
 
 /* Thread-local description of the last failure on this thread. */
 const char* aima_last_error(void);
 
-/* Library ABI version (major*100 + minor). */
+/* Library ABI version (major*100 + minor); 101 added the split up tensors of
+ * aima_moe_layer and aima_moe_grouped_prefill_ex. */
 int aima_version(void);
 
 /* Exact dequantization out[n][k] = f32(q - z) * f32(s) (bit-exact with the
@@ -97,6 +109,17 @@ int aima_version(void);
 int aima_u4_dequant(const uint8_t* qweight, const uint16_t* scale,
                     const uint8_t* zp, int64_t n, int64_t k, int32_t group,
                     float* out, void* stream);
+
+/* The same dequantization rounded once to f16: out[n][k] = f16(f32(q - z) *
+ * f32(s)) (round to nearest even, f16 subnormals kept), computed by the very
+ * routine that builds the grouped prefill GEMM's f16 MFMA weight operand --
+ * the weight form of the reference's f16 decompression path
+ * (engine/openvino/custom/iq36_fixed_fc_multi_output.cl:118-128 dequantizes
+ * in f32; OpenVINO's f16 inference precision rounds the product to f16).
+ * Same size rules as aima_u4_dequant; out 16-byte aligned. */
+int aima_u4_dequant_f16(const uint8_t* qweight, const uint16_t* scale,
+                        const uint8_t* zp, int64_t n, int64_t k, int32_t group,
+                        uint16_t* out, void* stream);
 
 /* Batch-1 U4 weight-only matvec y[n] = sum_k w[n][k] * x[k], f32 accumulate,
  * output f16 (round to nearest even) or f32.  Replaces the U4 fixed-FC op
@@ -258,13 +281,74 @@ int aima_moe_prefill_workspace_size(const aima_moe_layer* layer,
  * (engine/include/intel_qwen36/grouped_s8_u4_prefill_runtime.hpp:148-150,
  * top-k int32[T][8] + float[T*8] in, per-token routed sum out) and the
  * OpenVINO MOE3GemmFusedCompressed op
- * (engine/openvino/iq36-fixed-fc-moe-router-compat.patch:49-56).
- * Requires shared_inter == inter, hidden % 128 == 0, inter % 128 == 0. */
+ * (engine/openvino/iq36-fixed-fc-moe-router-compat.patch:49-56; gate and up
+ * may be separate tensors, see aima_moe_layer).  RunLayer's exact output (f32
+ * routed-only sum, strided top-k, f32 input) is aima_moe_grouped_prefill_ex.
+ * Requires group 128, shared_inter == inter, hidden % 256 == 0,
+ * inter % 128 == 0. */
 int aima_moe_grouped_prefill(const aima_moe_layer* layer, const uint16_t* x,
                              const uint16_t* residual, int64_t tokens,
                              const int32_t* ids, const float* weights,
                              int32_t k, uint16_t* out, void* workspace,
                              size_t workspace_bytes, void* stream);
+
+/* Output forms of aima_moe_grouped_prefill_ex. */
+#define AIMA_PREFILL_FULL_F16 0   /* f16 routed + sigmoid-gated shared (+ residual) */
+#define AIMA_PREFILL_ROUTED_F32 1 /* f32 routed sum only: RunLayer's output */
+
+/* Options of aima_moe_grouped_prefill_ex (zero-initialized = the defaults). */
+typedef struct aima_prefill_options {
+  int32_t output_mode;    /* AIMA_PREFILL_FULL_F16 (0) or AIMA_PREFILL_ROUTED_F32 */
+  int32_t input_f32;      /* 1: x is f32 [T][hidden], RunLayer's hidden_states type
+                             (rounded to f16 on the device); 0: x is f16 */
+  int64_t topk_stride;    /* bytes between consecutive tokens' int32 top-k rows
+                             (a multiple of 4, >= 4 * k); 0 = 4 * k (dense) */
+  void* stage_events[5];  /* optional hipEvent_t, recorded on `stream` before the
+                             schedule and after the schedule, the gate/up GEMM,
+                             the down GEMM and the combine (NULL entries skipped) */
+} aima_prefill_options;
+
+/* Grouped MoE FFN over T tokens with GroupedS8U4PrefillRuntime::RunLayer's
+ * contract (engine/include/intel_qwen36/grouped_s8_u4_prefill_runtime.hpp:62-84,
+ * 100-121; validation grouped_s8_u4_prefill_runtime.cpp:1040-1061):
+ *   topk     int32 ids, token t's k ids at byte offset t * topk_stride
+ *   weights  f32 [T*k] normalized router weights (RunLayer's router_weights)
+ *   x        f16 or (input_f32) f32 hidden states [T][hidden]
+ *   out      AIMA_PREFILL_ROUTED_F32: f32 [T][hidden],
+ *              out[t] = sum_r f32(f16(w_r * down_r(swiglu(gate_up_r x_t))))
+ *              summed in rank order from 0 (the reference's grouped output,
+ *              grouped_s8_u4_f16_contribution_moe.cl:831-845); no shared
+ *              expert (its tensors may be NULL) and no residual;
+ *            AIMA_PREFILL_FULL_F16: f16 [T][hidden] as aima_moe_grouped_prefill.
+ * Out-of-range or duplicated ids set the workspace error word (RunLayer
+ * throws).  Workspace as aima_moe_prefill_workspace_size; the schedule, the
+ * weighted SwiGLU rows and the contributions of the call stay in it (see
+ * aima_moe_prefill_workspace_views). */
+int aima_moe_grouped_prefill_ex(const aima_moe_layer* layer, const void* x,
+                                const uint16_t* residual, int64_t tokens,
+                                const int32_t* topk, const float* weights, int32_t k,
+                                void* out, const aima_prefill_options* options,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device pointers into a prefill workspace: the intermediates the last
+ * aima_moe_grouped_prefill(_ex) call on it left there (RunLayer's
+ * capture_intermediates outputs, grouped_s8_u4_prefill_runtime.hpp:100-121).
+ * Rows are in schedule order (expert-major, tokens ascending within an
+ * expert); routed rows 0 .. T*k-1, then (full mode) the shared expert's rows
+ * T*k + t. */
+typedef struct aima_prefill_views {
+  int32_t* offsets;          /* [experts] exclusive end row of each expert */
+  int32_t* token_map;        /* [T*k] source token of each routed row */
+  int32_t* inverse_map;      /* [T*k] row of (token, rank) */
+  float* compact_weights;    /* [T*k] router weight of each routed row */
+  uint16_t* weighted_swiglu; /* f16 [T*k + T][inter]: w_row * silu(gate) * up */
+  uint16_t* contributions;   /* f16 [T*k + T][hidden]: down of the row above */
+  int32_t* tiles;            /* [tile_count][4] expert, first row, rows, 0 */
+  int32_t* tile_count;       /* one int */
+} aima_prefill_views;
+int aima_moe_prefill_workspace_views(const aima_moe_layer* layer, int64_t tokens,
+                                     int32_t k, void* workspace,
+                                     aima_prefill_views* views);
 
 /* Workspace bytes for aima_grouped_schedule. */
 int aima_grouped_schedule_workspace_size(int64_t tokens, int32_t k,

@@ -81,6 +81,8 @@ def lib():
         L.orc_moe_ffn_token_detail.argtypes = [C.c_void_p] * 16
         L.orc_moe_ffn_tokens.argtypes = [C.c_void_p, _i64, C.c_void_p, C.c_void_p,
                                          C.c_void_p, C.c_void_p, _i64, C.c_void_p, _i64]
+        L.orc_moe_routed_tokens.argtypes = [C.c_void_p, _i64, C.c_void_p, C.c_void_p,
+                                            C.c_void_p, _i64, C.c_void_p, _i64]
         L.orc_moe_ffn_decode_threaded.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p,
                                                   C.c_void_p, C.c_void_p, _i64,
                                                   C.c_void_p, _i64]
@@ -455,6 +457,24 @@ def moe_ffn_tokens(mw: MoeWeights, x, ids, w, residual=None, threads: int = 8) -
                                   w.ctypes.data, ids.shape[1], out.ctypes.data, threads)
     del keep
     _check(rc, "moe_ffn_tokens")
+    return out
+
+
+def moe_routed_tokens(mw: MoeWeights, x, ids, w, threads: int = 8) -> np.ndarray:
+    """Routed sum only, sum_r w_r * down_r(swiglu(gate_up_r x)), per token:
+    the output of the reference's grouped RunLayer
+    (grouped_s8_u4_prefill_runtime.hpp:100-121) with the CPU arithmetic of
+    apply_expert_weights / aggregate_experts (gguf_loader.cpp:3773-3819)."""
+    x = _f32(x)
+    T = x.shape[0]
+    ids = np.ascontiguousarray(ids, np.int32)
+    w = _f32(w)
+    out = np.empty((T, mw.hidden), np.float32)
+    cs, keep = mw._c()
+    rc = lib().orc_moe_routed_tokens(C.addressof(cs), T, x.ctypes.data, ids.ctypes.data,
+                                     w.ctypes.data, ids.shape[1], out.ctypes.data, threads)
+    del keep
+    _check(rc, "moe_routed_tokens")
     return out
 
 

@@ -464,13 +464,15 @@ typedef struct {
   float* ffn_out;     /* [hidden] */
 } orc_moe_scratch;
 
-/* x: expert input (ffn_norm), f32 [hidden]; residual: f32 [hidden] or NULL
- * (then out = ffn_out).  ids/w: k selected experts and normalized weights. */
-static int moe_ffn_token(const orc_moe_weights* mw, const float* x,
-                         const float* residual, const int32_t* ids,
-                         const float* w, int64_t k, float* out,
-                         orc_moe_scratch* s) {
-  const int64_t H = mw->hidden, I = mw->inter, IS = mw->shared_inter;
+/* The routed half of the layer: s->moe_out = aggregate_experts(
+ * apply_expert_weights(down_r(swiglu(gate_up_r x)), w)) -- the expert part of
+ * run_qwen36_moe_ffn_layer (gguf_loader.cpp:5711-5738) and the output of the
+ * reference's grouped prefill RunLayer (grouped_s8_u4_prefill_runtime.hpp:
+ * 100-121, routed sum only). */
+static int moe_routed_token(const orc_moe_weights* mw, const float* x,
+                            const int32_t* ids, const float* w, int64_t k,
+                            orc_moe_scratch* s) {
+  const int64_t H = mw->hidden, I = mw->inter;
   for (int64_t r = 0; r < k; ++r) {
     if (ids[r] < 0 || ids[r] >= mw->gate_up.experts) return ORC_ERANGE;
   }
@@ -483,6 +485,18 @@ static int moe_ffn_token(const orc_moe_weights* mw, const float* x,
   }
   orc_apply_expert_weights(s->down, w, k, H, s->weighted);
   orc_aggregate_experts(s->weighted, k, H, s->moe_out);
+  return ORC_OK;
+}
+
+/* x: expert input (ffn_norm), f32 [hidden]; residual: f32 [hidden] or NULL
+ * (then out = ffn_out).  ids/w: k selected experts and normalized weights. */
+static int moe_ffn_token(const orc_moe_weights* mw, const float* x,
+                         const float* residual, const int32_t* ids,
+                         const float* w, int64_t k, float* out,
+                         orc_moe_scratch* s) {
+  const int64_t H = mw->hidden, IS = mw->shared_inter;
+  const int rc = moe_routed_token(mw, x, ids, w, k, s);
+  if (rc != ORC_OK) return rc;
 
   expert_matvec(&mw->shared_gate_up, 0, x, s->shared_gate_up);
   orc_swiglu_pair(s->shared_gate_up, s->shared_gate_up + IS, IS, s->shared_swiglu);
@@ -588,6 +602,7 @@ typedef struct {
   const float* w;        /* [T][k] */
   int64_t k;
   float* out;            /* [T][H] */
+  int routed_only;       /* out = the routed sum only */
   int rc;
   pthread_mutex_t lock;
 } tokens_ctx;
@@ -599,10 +614,15 @@ static void tokens_range(void* p, int64_t begin, int64_t end) {
   int rc = ORC_OK;
   if (!scratch_alloc(c->mw, c->k, &s)) rc = ORC_ERUNTIME;
   for (int64_t t = begin; t < end && rc == ORC_OK; ++t) {
-    rc = moe_ffn_token(c->mw, c->x + t * H,
-                       c->residual ? c->residual + t * H : NULL,
-                       c->ids + t * c->k, c->w + t * c->k, c->k,
-                       c->out + t * H, &s);
+    if (c->routed_only) {
+      rc = moe_routed_token(c->mw, c->x + t * H, c->ids + t * c->k, c->w + t * c->k, c->k, &s);
+      if (rc == ORC_OK) memcpy(c->out + t * H, s.moe_out, sizeof(float) * (size_t)H);
+    } else {
+      rc = moe_ffn_token(c->mw, c->x + t * H,
+                         c->residual ? c->residual + t * H : NULL,
+                         c->ids + t * c->k, c->w + t * c->k, c->k,
+                         c->out + t * H, &s);
+    }
   }
   scratch_free(&s);
   if (rc != ORC_OK) {
@@ -630,6 +650,28 @@ int orc_moe_ffn_tokens(const orc_moe_weights* mw, int64_t tokens,
   c.w = w;
   c.k = k;
   c.out = out;
+  c.routed_only = 0;
+  c.rc = ORC_OK;
+  pthread_mutex_init(&c.lock, NULL);
+  orc_parallel_for_rows(tokens, threads, tokens_range, &c);
+  pthread_mutex_destroy(&c.lock);
+  return c.rc;
+}
+
+/* T tokens, routed sum only (RunLayer's f32 output), token-parallel. */
+int orc_moe_routed_tokens(const orc_moe_weights* mw, int64_t tokens,
+                          const float* x, const int32_t* ids, const float* w,
+                          int64_t k, float* out, int64_t threads) {
+  if (!moe_weights_ok(mw) || k <= 0 || tokens < 0) return ORC_EINVAL;
+  tokens_ctx c;
+  c.mw = mw;
+  c.x = x;
+  c.residual = NULL;
+  c.ids = ids;
+  c.w = w;
+  c.k = k;
+  c.out = out;
+  c.routed_only = 1;
   c.rc = ORC_OK;
   pthread_mutex_init(&c.lock, NULL);
   orc_parallel_for_rows(tokens, threads, tokens_range, &c);

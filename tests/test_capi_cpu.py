@@ -40,7 +40,7 @@ def test_library_shares_torch_hip_runtime(pkg):
 
 def test_version_and_error_paths(pkg):
     L = pkg._lib.lib()
-    assert L.aima_version() == 100
+    assert L.aima_version() == 101
     rc = L.aima_u4_matvec(None, None, None, None, 4, 2048, 128, None, 0, None)
     assert rc == pkg._lib.AIMA_E_INVALID
     assert b"null pointer" in L.aima_last_error()
@@ -184,3 +184,119 @@ def test_prefill_rejects_batches_past_the_offset_limit(pkg):
         rc = lib.aima_moe_grouped_prefill(C.byref(lc), p, None, T, p, p, 8, p, p, 1 << 40, None)
         assert rc == L.AIMA_E_INVALID, T
         assert b"2^30" in lib.aima_last_error()
+
+
+def test_run_layer_entry_validation(pkg):
+    """aima_moe_grouped_prefill_ex (RunLayer's contract) checks its options,
+    the top-k stride and the split tensors before any launch."""
+    L = pkg._lib
+    lib = L.lib()
+    p = C.c_void_p(1 << 20)
+    lc = _fake_layer(pkg)
+    opt = L.PrefillOptionsC()
+    opt.output_mode = L.AIMA_PREFILL_ROUTED_F32
+
+    def call(layer=lc, o=opt, residual=None, topk=p, ws_bytes=1 << 40):
+        return lib.aima_moe_grouped_prefill_ex(C.byref(layer), p, residual, 64, topk, p, 8, p,
+                                               C.byref(o), p, ws_bytes, None)
+
+    assert call(ws_bytes=16) == L.AIMA_E_WORKSPACE  # everything else valid
+    opt.topk_stride = 28  # < 4 * k
+    assert call() == L.AIMA_E_INVALID and b"topk_stride" in lib.aima_last_error()
+    opt.topk_stride = 34  # not a multiple of 4
+    assert call() == L.AIMA_E_INVALID
+    opt.topk_stride = 48
+    assert call(ws_bytes=16) == L.AIMA_E_WORKSPACE
+    assert call(topk=C.c_void_p((1 << 20) + 2)) == L.AIMA_E_INVALID  # misaligned ids
+    assert call(residual=p) == L.AIMA_E_INVALID  # routed output takes no residual
+    bad = L.PrefillOptionsC()
+    bad.output_mode = 5
+    assert call(o=bad) == L.AIMA_E_INVALID
+    bad.output_mode, bad.input_f32 = 0, 2
+    assert call(o=bad) == L.AIMA_E_INVALID
+    # routed-only needs no shared expert tensors
+    noshared = _fake_layer(pkg)
+    noshared.shared_gate_up = L.U4TensorC(None, None, None)
+    noshared.shared_down = L.U4TensorC(None, None, None)
+    noshared.shared_gate_vec = None
+    assert call(layer=noshared, ws_bytes=16) == L.AIMA_E_WORKSPACE
+    full = L.PrefillOptionsC()
+    assert call(layer=noshared, o=full) == L.AIMA_E_INVALID
+    # a split up tensor must be complete
+    half = _fake_layer(pkg)
+    half.up = L.U4TensorC(1 << 20, None, 1 << 20)
+    assert call(layer=half) == L.AIMA_E_INVALID
+    assert lib.aima_moe_ffn_decode(C.byref(half), p, None, p, p, 8, p, p, 1 << 30, None) == \
+        L.AIMA_E_INVALID
+    ok_split = _fake_layer(pkg)
+    ok_split.up = L.U4TensorC(1 << 20, 1 << 20, 1 << 20)
+    ok_split.shared_up = L.U4TensorC(1 << 20, 1 << 20, 1 << 20)
+    assert call(layer=ok_split, ws_bytes=16) == L.AIMA_E_WORKSPACE
+
+
+def test_stack_prefill_requires_aligned_norm(pkg):
+    """The fused combine reads the next layer's norm weights as 16-byte
+    vectors, so the stack entry checks their alignment."""
+    L = pkg._lib
+    lib = L.lib()
+    p = C.c_void_p(1 << 20)
+    lc = _fake_layer(pkg)
+    lc.norm_weight = (1 << 20) + 4
+    rc = lib.aima_moe_stack_prefill(C.byref(lc), 1, 1e-6, p, 64, p, p, 8, p, p, 1 << 40, None)
+    assert rc == L.AIMA_E_INVALID and b"norm_weight" in lib.aima_last_error()
+
+
+def test_prefill_workspace_views(pkg):
+    """The views point into the workspace, in its layout order, without
+    overlapping, and end inside the size the size query reports."""
+    L = pkg._lib
+    lc = _fake_layer(pkg)
+    T, k = 2048, 8
+    size = L.size_query("aima_moe_prefill_workspace_size", C.byref(lc), T, k)
+    base = 1 << 30
+    v = L.PrefillViewsC()
+    L.call("aima_moe_prefill_workspace_views", C.byref(lc), T, k, C.c_void_p(base), C.byref(v))
+    A = T * k
+    spans = [(v.offsets, 256 * 4), (v.tiles, 16), (v.token_map, A * 4), (v.inverse_map, A * 4),
+             (v.compact_weights, A * 4), (v.weighted_swiglu, (A + T) * 512 * 2),
+             (v.contributions, (A + T) * 2048 * 2)]
+    end = base
+    for ptr, n in spans:
+        assert ptr >= end and ptr % 256 == 0
+        end = ptr + n
+    assert end <= base + size
+    assert base <= v.tile_count < v.offsets
+
+
+def test_dequant_f16_validation(pkg):
+    L = pkg._lib
+    lib = L.lib()
+    p = C.c_void_p(1 << 20)
+    assert lib.aima_u4_dequant_f16(p, p, p, 4, 256, 128, None, None) == L.AIMA_E_INVALID
+    assert lib.aima_u4_dequant_f16(p, p, p, 4, 256, 100, p, None) == L.AIMA_E_INVALID
+    assert lib.aima_u4_dequant_f16(p, p, p, 4, 256, 128, C.c_void_p((1 << 20) + 8), None) == \
+        L.AIMA_E_INVALID  # out must be 16-byte aligned
+
+
+def test_split_layout_round_trip(pkg):
+    """to_split() keeps every gate and up row, scale and zero point."""
+    layer = pkg.synth.moe_layer(hidden=256, inter=128, experts=4, seed=5, device="cpu")
+    sp = layer.to_split()
+    assert sp.split and sp.inter == 128 and sp.shared_inter == 128
+    G = 2
+    q = layer.gate_up.qweight
+    assert torch.equal(sp.gate_up.qweight, q[:, :128]) and torch.equal(sp.up.qweight, q[:, 128:])
+    assert torch.equal(sp.up.scale, layer.gate_up.scale[:, 128:])
+
+    def nibbles(z, rows):
+        z = z.reshape(z.shape[0] if z.dim() > 1 else 1, -1)
+        return torch.stack([z & 15, z >> 4], -1).reshape(z.shape[0], rows, G)
+
+    zc = nibbles(layer.gate_up.zp, 256)
+    assert torch.equal(nibbles(sp.gate_up.zp, 128), zc[:, :128])
+    assert torch.equal(nibbles(sp.up.zp, 128), zc[:, 128:])
+    zs = nibbles(layer.shared_gate_up.zp, 256)
+    assert torch.equal(nibbles(sp.shared_up.zp, 128), zs[:, 128:])
+    assert sp.expert_bytes() == layer.expert_bytes()
+    c = sp.c()
+    assert c.up.qweight == sp.up.qweight.data_ptr() and layer.c().up.qweight is None

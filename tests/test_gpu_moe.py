@@ -192,7 +192,8 @@ def test_prefill_runtime_contract(pkg, dev, layer_small):
     x = pkg.synth.activations(T, layer.hidden, 5, dev)
     ids, w = pkg.select_router_topk(pkg.synth.router_logits(T, 16, 6, dev), 8)
     run = rt.RunLayer(h, pkg.GroupedU4PrefillInput(x, ids, w, warmup=1, repeat=3,
-                                                   capture_intermediates=True))
+                                                   capture_intermediates=True,
+                                                   include_shared=True))
     assert len(run.timing.samples_us) == 3 and run.timing.minimum_us > 0
     assert run.active_experts > 0 and run.max_group_size > 0
     ref = oracle.moe_ffn_tokens(mw, f16_to_f32(x), ids.cpu().numpy(), w.cpu().numpy(),
@@ -201,7 +202,7 @@ def test_prefill_runtime_contract(pkg, dev, layer_small):
     st = rt.stats()
     assert st["run_count"] == 1 and st["layer_count"] == 1
     with pytest.raises(KeyError):
-        rt.RunLayer(99, pkg.GroupedU4PrefillInput(x, ids, w))
+        rt.RunLayer(99, pkg.GroupedU4PrefillInput(x, ids, w, include_shared=True))
 
 
 def test_decode_phases_compose(pkg, dev, layer_full):
