@@ -88,59 +88,132 @@ def graphed(torch, fn):
     return g.replay
 
 
-def cpu_baseline(torch, pkg, oracle, layers, x, ids, w, budget_s=12.0):
-    """The oracle's threaded decode (row-parallel matvecs, the reference CPU
-    pattern) through all 40 layers for the decode token, repeated within a
-    time budget.  Only the experts the token selects are copied to the host."""
-    from tests.helpers import f16_bits, u4_to_oracle
+def _host_u4(t, idx=None):
+    """Device U4 weight (optionally experts idx only) -> numpy (q, s, z) per expert."""
+    import numpy as np
+    import torch
 
-    threads = min(16, os.cpu_count() or 1)
-    ids_np = ids.cpu().numpy()
-    w_np = w.cpu().numpy()
-    host = []
-    for L, layer in enumerate(layers):
-        idx = torch.as_tensor(ids_np[L].astype("int64"), device=layer.gate_up.qweight.device)
+    q, sc, z = t.qweight, t.scale, t.zp
+    if idx is not None:
+        ii = torch.as_tensor([int(i) for i in idx], dtype=torch.int64, device=q.device)
+        q, sc, z = q.index_select(0, ii), sc.index_select(0, ii), z.index_select(0, ii)
+    q = q.cpu().numpy()
+    sc = sc.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    z = z.cpu().numpy()
+    if idx is None:
+        return [(q.reshape(t.rows, -1), sc.reshape(t.rows, -1), z.reshape(-1))]
+    return [(q[i], sc[i], z[i]) for i in range(len(idx))]
 
-        def pick(t):
-            return u4_to_oracle(type(t)(t.qweight.index_select(0, idx).contiguous(),
-                                        t.scale.index_select(0, idx).contiguous(),
-                                        t.zp.index_select(0, idx).contiguous(),
-                                        t.rows, t.k, t.group))
 
-        host.append((oracle.MoeWeights(pick(layer.gate_up), pick(layer.down),
-                                       u4_to_oracle(layer.shared_gate_up),
-                                       u4_to_oracle(layer.shared_down),
-                                       f16_bits(layer.shared_gate_vec)),
-                     layer.norm_weight.cpu().numpy()))
+def _stats(samples):
+    srt = sorted(samples)
+    return {"min": round(srt[0], 3), "median": round(srt[len(srt) // 2], 3),
+            "mean": round(sum(srt) / len(srt), 3), "repeats": len(srt)}
+
+
+def _time_cpu(fn, min_s=0.6, min_reps=3):
+    fn()  # warm
+    samples = []
+    t_end = time.perf_counter() + min_s
+    while time.perf_counter() < t_end or len(samples) < min_reps:
+        t0 = time.perf_counter()
+        fn()
+        samples.append((time.perf_counter() - t0) * 1e6)
+    return samples
+
+
+def cpu_baseline(torch, pkg, layers, x, ids, w, dev):
+    """The reference CPU path (oracle/cpu_baseline.c: the row-parallel U4
+    matvec and MoE layer of gguf_loader.cpp, scale / zero point hoisted per
+    group, OpenMP) compiled here with -O3 -march=native, at 1 thread and at
+    this process's CPU share, for configs 0, 1, 2, 3, 4a and 4b.  Only the
+    experts a sample touches are copied to the host."""
+    import tempfile
+
     import numpy as np
 
-    local_ids = np.arange(K_TOP, dtype=np.int32)
-    x_bits = f16_bits(x)
+    from oracle import cpu_baseline as cpb
 
-    def one_token():
-        r = x_bits
-        for L, (mw, nw) in enumerate(host):
-            rf = oracle.f16_values(r)
-            h = oracle.f16_values(oracle.float_to_half(oracle.rms_norm(rf, nw, EPS)))
-            o = oracle.moe_ffn_decode_threaded(mw, h, local_ids, w_np[L], residual=rf,
-                                               threads=threads)
-            r = oracle.float_to_half(o)
+    base = cpb.load(tempfile.mkdtemp(prefix="aima_cpb_"))
+    share = len(os.sched_getaffinity(0))
+    nthreads = max(1, min(16, share))  # the box grants one GPU 16 host cores
+    gen = pkg.synth.generator(0, dev)
+    m0 = pkg.synth.u4_weight(1, 4096, 2048, GROUP, gen, dev)
+    m3 = pkg.synth.u4_weight(1, 248320, 2048, GROUP, pkg.synth.generator(3, dev), dev)
+    mats = {"config0": (_host_u4(m0)[0], 4096), "config3": (_host_u4(m3)[0], 248320)}
+    del m3
+    xv = np.random.default_rng(0).normal(size=2048).astype(np.float32)
+    x_np = x.float().cpu().numpy()
+    ids_np, w_np = ids.cpu().numpy(), w.cpu().numpy()
+
+    def layer_rec(L, sel):
+        lay = layers[L]
+        ex = list(zip(_host_u4(lay.gate_up, sel), _host_u4(lay.down, sel)))
+        sh = (_host_u4(lay.shared_gate_up)[0], _host_u4(lay.shared_down)[0])
+        return base.layer(ex, sh, lay.shared_gate_vec.float().cpu().numpy(),
+                          lay.norm_weight.cpu().numpy(), H, I, GROUP)
+
+    decode_layers = [(layer_rec(L, ids_np[L]), w_np[L]) for L in range(LAYERS)]
+    # prefill samples: config 2 (one layer, Zipf routing) token by token, and
+    # config 4b (40 layers, uniform routing) for two tokens
+    T2 = 16
+    xs2 = pkg.synth.activations(2048, H, 2, dev)[:T2].float().cpu().numpy()
+    i2, w2 = pkg.select_router_topk(pkg.synth.router_logits(2048, E, 3, dev, zipf_s=1.1), K_TOP)
+    i2, w2 = i2[:T2].cpu().numpy(), w2[:T2].cpu().numpy()
+    p2 = [(layer_rec(0, i2[t]), w2[t]) for t in range(T2)]
+    T4 = 2
+    xs4 = pkg.synth.activations(16384, H, 43, dev)[:T4].float().cpu().numpy()
+    lg4 = torch.stack([pkg.synth.router_logits(16384, E, 2044 + l, dev)[:T4] for l in range(LAYERS)])
+    i4, w4 = pkg.select_router_topk(lg4, K_TOP)
+    i4, w4 = i4.cpu().numpy(), w4.cpu().numpy()
+    p4 = [[(layer_rec(L, i4[L, t]), w4[L, t]) for L in range(LAYERS)] for t in range(T4)]
+
+    out = np.empty(H, np.float32)
+
+    def stack(r0, recs):
+        r, nxt = r0.copy(), np.empty_like(r0)
+        for lay, wl in recs:
+            base.moe_token(lay, wl, EPS, r, nxt)
+            r, nxt = nxt, r
         return r
 
-    one_token()  # warm
-    samples = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end or len(samples) < 3:
-        t0 = time.perf_counter()
-        one_token()
-        samples.append((time.perf_counter() - t0) * 1e6)
-    samples.sort()
-    return {"value": samples[len(samples) // 2], "unit": "us/token", "cores": threads,
-            "kind": "port", "min": samples[0], "mean": sum(samples) / len(samples),
-            "sample": f"{len(samples)} decode tokens through all 40 layers (8 routed + shared "
-                      f"expert per layer, U4 dequant + sequential f32 dots, row-parallel over "
-                      f"{threads} threads); median reported",
-            "host_cpu": _cpu_model()}
+    def mv(name):
+        (q, sc, z), n = mats[name]
+        y = np.empty(n, np.float32)
+        return lambda: base.matvec(q, sc, z, n, 2048, GROUP, xv, y)
+
+    work = {
+        "config0_matvec_K2048_N4096": ("us/matvec", mv("config0"), 1),
+        "config1_decode_layer": ("us/token", lambda: base.moe_token(decode_layers[0][0],
+                                                                     decode_layers[0][1], EPS,
+                                                                     x_np, out), 1),
+        "config2_prefill_T2048": ("tok/s", lambda: [base.moe_token(l_, w_, EPS, xs2[t], out)
+                                                     for t, (l_, w_) in enumerate(p2)], T2),
+        "config3_lm_head_N248320": ("us/matvec", mv("config3"), 1),
+        "config4a_decode_40L": ("us/token", lambda: stack(x_np, decode_layers), 1),
+        "config4b_prefill_40L_T16384": ("tok/s", lambda: [stack(xs4[t], p4[t])
+                                                          for t in range(T4)], T4),
+    }
+    recs = {}
+    for name, (unit, fn, ntok) in work.items():
+        rec = {"unit": unit}
+        for th in sorted({1, nthreads}):
+            base.set_threads(th)
+            st = _stats(_time_cpu(fn))
+            if unit == "tok/s":
+                st = {"tok_s": round(ntok / (st["median"] * 1e-6), 2), "us_per_call": st,
+                      "tokens_per_call": ntok}
+            rec[f"threads_{th}"] = st
+        recs[name] = rec
+        log(f"cpu baseline {name}: {rec}")
+    head = recs["config4a_decode_40L"][f"threads_{nthreads}"]
+    return {"value": head["median"], "unit": "us/token", "cores": nthreads, "kind": "port",
+            "sample": f"config 4a: one decode token through all 40 layers (8 routed + shared "
+                      f"expert per layer), median of {head['repeats']}; every config at 1 and "
+                      f"{nthreads} threads in 'configs' (prefill configs token by token, the "
+                      f"reference CPU layer function: {T2} tokens of config 2, {T4} of 4b)",
+            "build": "gcc -O3 -march=native -fopenmp (built on this host)",
+            "host_cpu": _cpu_model(), "host_cpus_visible": share, "configs": recs}
 
 
 def profiled_traffic(kernel):
@@ -282,6 +355,7 @@ def main():
     # algorithmic bytes are the 8 routed + 1 shared experts of all 40 layers
     # plus the activations, timed back to back on the launch stream
     per_launch_us = timed(torch, decode_step, args.steps, warmup=3)
+    plan.check()  # every timed launch finished without a device error
     achieved = (weight_bytes + act_bytes) / per_launch_us / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
@@ -312,15 +386,36 @@ def main():
     }
 
     if not args.no_extras:
-        result["prefill"] = prefill_bench(torch, pkg, ops, synth, layers, layers_c, dev)
+        pf = prefill_bench(torch, pkg, ops, synth, layers, layers_c, dev)
+        result["prefill"] = pf
+        # the prefill half of the metric as flat scalars
+        c2, c4 = pf["config2_T2048"], pf["config4b_T16384_40L"]
+        result.update({"prefill_T2048_us": c2["us"], "prefill_T2048_tok_s": c2["tok_s"],
+                       "prefill_T2048_mfma_frac": c2["mfma_frac"],
+                       "prefill_4b_ms": round(c4["us"] / 1e3, 3),
+                       "prefill_4b_tok_s": c4["tok_s"], "prefill_4b_mfma_frac": c4["mfma_frac"]})
         result["configs"] = matvec_bench(torch, ops, synth, layers, layers_c, dev, ids_buf,
                                          w_buf)
 
     if not args.no_cpu_baseline:
-        import oracle
-
-        log("cpu baseline (oracle, 40-layer decode token)")
-        result["cpu_baseline"] = cpu_baseline(torch, pkg, oracle, layers, x, ids_buf, w_buf)
+        log("cpu baseline (reference CPU path, all configs, 1 and N threads)")
+        cb = cpu_baseline(torch, pkg, layers, x, ids_buf, w_buf, dev)
+        result["cpu_baseline"] = cb
+        # each CPU record beside the GPU's number for the same config
+        gpu = {"config4a_decode_40L": (step_us, roofline["frac"])}
+        if not args.no_extras:
+            cf = result["configs"]
+            gpu.update({
+                "config0_matvec_K2048_N4096": (cf["config0_matvec_K2048_N4096"]["us"],
+                                               cf["config0_matvec_K2048_N4096"]["hbm_frac"]),
+                "config1_decode_layer": (cf["config1_decode_layer"]["us"],
+                                         cf["config1_decode_layer"]["hbm_frac"]),
+                "config3_lm_head_N248320": (cf["config3_lm_head_N248320"]["us"],
+                                            cf["config3_lm_head_N248320"]["hbm_frac"]),
+                "config2_prefill_T2048": (c2["tok_s"], c2["mfma_frac"]),
+                "config4b_prefill_40L_T16384": (c4["tok_s"], c4["mfma_frac"])})
+        for name, (v, frac) in gpu.items():
+            cb["configs"][name]["gpu"] = {"value": v, "roofline_frac": frac}
     print(json.dumps(result), flush=True)
 
 
