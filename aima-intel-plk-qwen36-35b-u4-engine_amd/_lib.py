@@ -102,6 +102,8 @@ SIGNATURES = {
                                         C.c_size_t, _vp]),
     "aima_moe_stack_decode_routed": (C.c_int, [_LP, C.POINTER(U4TensorC), _i32, _f32, _vp, _i32,
                                                _f32, _vp, _vp, _vp, _vp, C.c_size_t, _vp]),
+    "aima_moe_stack_decode_routed_noalloc": (C.c_int, [_LP, C.POINTER(U4TensorC), _i32, _f32, _vp,
+                                                       _i32, _f32, _vp, _vp, _vp, _vp, _vp]),
     "aima_moe_stack_prefill_workspace_size": (C.c_int, [_LP, _i64, _i32, _szp]),
     "aima_moe_stack_prefill": (C.c_int, [_LP, _i32, _f32, _vp, _i64, _vp, _vp, _i32, _vp, _vp,
                                          C.c_size_t, _vp]),

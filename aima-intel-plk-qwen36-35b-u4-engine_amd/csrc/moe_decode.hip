@@ -17,6 +17,9 @@
 
 #include <math.h>
 
+#include <mutex>
+#include <unordered_map>
+
 namespace aima {
 
 constexpr int kPairsPerWave = 2;
@@ -540,12 +543,11 @@ extern "C" int aima_moe_stack_decode(const aima_moe_layer* layers, int32_t n_lay
   return AIMA_OK;
 }
 
-extern "C" int aima_moe_stack_decode_routed(const aima_moe_layer* layers,
-                                            const aima_u4_tensor* routers, int32_t n_layers,
-                                            float eps, const uint16_t* residual_in, int32_t k,
-                                            float min_weight_sum, int32_t* ids, float* weights,
-                                            uint16_t* out, void* workspace,
-                                            size_t workspace_bytes, void* stream) {
+// Argument checks of the routed stack decode (both entry points).
+static int check_routed_stack(const aima_moe_layer* layers, const aima_u4_tensor* routers,
+                              int32_t n_layers, const uint16_t* residual_in, int32_t k,
+                              float min_weight_sum, int32_t* ids, float* weights,
+                              uint16_t* out) {
   AIMA_REQUIRE(layers && routers && n_layers > 0, "moe_stack_decode_routed: need layers");
   AIMA_REQUIRE(residual_in && ids && weights && out, "moe_stack_decode_routed: null pointer");
   AIMA_REQUIRE(min_weight_sum > 0.f, "moe_stack_decode_routed: minimum weight sum must be positive");
@@ -565,13 +567,14 @@ extern "C" int aima_moe_stack_decode_routed(const aima_moe_layer* layers,
   if (!decode_shape_ok(&layers[0])) {
     return fail(AIMA_E_UNSUPPORTED, "moe_stack_decode_routed: unsupported hidden/inter");
   }
-  const size_t need = decode_ws_bytes(layers[0].hidden, layers[0].inter, k, true);
-  if (!workspace || workspace_bytes < need) {
-    return fail(AIMA_E_WORKSPACE, "moe_stack_decode_routed: workspace missing or too small");
-  }
-  AIMA_REQUIRE(aligned(workspace, 256), "moe_stack_decode_routed: workspace must be 256-byte aligned");
-  const DecodeWs w = decode_ws(workspace, layers[0].hidden, layers[0].inter, k, true);
-  hipStream_t st = (hipStream_t)stream;
+  return AIMA_OK;
+}
+
+// The routed stack decode's launches on workspace w (its error word is w.err).
+static int routed_stack_run(const aima_moe_layer* layers, const aima_u4_tensor* routers,
+                            int32_t n_layers, float eps, const uint16_t* residual_in, int32_t k,
+                            float min_weight_sum, int32_t* ids, float* weights, uint16_t* out,
+                            const DecodeWs& w, hipStream_t st) {
   const uint16_t* r = residual_in;
   for (int32_t l = 0; l < n_layers; ++l) {
     const aima_moe_layer& L = layers[l];
@@ -591,4 +594,81 @@ extern "C" int aima_moe_stack_decode_routed(const aima_moe_layer* layers,
     r = dst;
   }
   return AIMA_OK;
+}
+
+extern "C" int aima_moe_stack_decode_routed(const aima_moe_layer* layers,
+                                            const aima_u4_tensor* routers, int32_t n_layers,
+                                            float eps, const uint16_t* residual_in, int32_t k,
+                                            float min_weight_sum, int32_t* ids, float* weights,
+                                            uint16_t* out, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  int rc = check_routed_stack(layers, routers, n_layers, residual_in, k, min_weight_sum, ids,
+                              weights, out);
+  if (rc != AIMA_OK) return rc;
+  const size_t need = decode_ws_bytes(layers[0].hidden, layers[0].inter, k, true);
+  if (!workspace || workspace_bytes < need) {
+    return fail(AIMA_E_WORKSPACE, "moe_stack_decode_routed: workspace missing or too small");
+  }
+  AIMA_REQUIRE(aligned(workspace, 256), "moe_stack_decode_routed: workspace must be 256-byte aligned");
+  const DecodeWs w = decode_ws(workspace, layers[0].hidden, layers[0].inter, k, true);
+  return routed_stack_run(layers, routers, n_layers, eps, residual_in, k, min_weight_sum, ids,
+                          weights, out, w, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free routed stack decode: the workspace is a fixed device array
+// of this library (one copy per GPU, kept until the process ends) instead of
+// caller memory.  Host code never uses the array's name as an address: the
+// device address comes from hipGetSymbolAddress, once per device, with that
+// device current.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kNoAllocScratchBytes = 128 * 1024;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mu;
+std::unordered_map<int, void*> g_scratch_ptr;  // device ordinal -> address of `scratch`
+
+int scratch_address(void** ptr) {
+  int dev = 0;
+  AIMA_HIP(hipGetDevice(&dev));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  auto it = g_scratch_ptr.find(dev);
+  if (it == g_scratch_ptr.end()) {
+    void* p = nullptr;
+    AIMA_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    it = g_scratch_ptr.emplace(dev, p).first;
+  }
+  *ptr = it->second;
+  return AIMA_OK;
+}
+
+}  // namespace
+
+extern "C" int aima_moe_stack_decode_routed_noalloc(const aima_moe_layer* layers,
+                                                    const aima_u4_tensor* routers,
+                                                    int32_t n_layers, float eps,
+                                                    const uint16_t* residual_in, int32_t k,
+                                                    float min_weight_sum, int32_t* ids,
+                                                    float* weights, uint16_t* out,
+                                                    uint32_t* error_word, void* stream) {
+  int rc = check_routed_stack(layers, routers, n_layers, residual_in, k, min_weight_sum, ids,
+                              weights, out);
+  if (rc != AIMA_OK) return rc;
+  AIMA_REQUIRE(error_word != nullptr, "moe_stack_decode_routed_noalloc: null error word");
+  const size_t need = decode_ws_bytes(layers[0].hidden, layers[0].inter, k, true);
+  if (need > kNoAllocScratchBytes) {
+    return fail(AIMA_E_UNSUPPORTED,
+                "moe_stack_decode_routed_noalloc: this shape needs " + std::to_string(need) +
+                    " scratch bytes, more than the fixed " +
+                    std::to_string(kNoAllocScratchBytes) + " (use aima_moe_stack_decode_routed)");
+  }
+  void* base = nullptr;
+  rc = scratch_address(&base);
+  if (rc != AIMA_OK) return rc;
+  DecodeWs w = decode_ws(base, layers[0].hidden, layers[0].inter, k, true);
+  w.err = error_word;  // device errors go to the caller's word, never cleared here
+  return routed_stack_run(layers, routers, n_layers, eps, residual_in, k, min_weight_sum, ids,
+                          weights, out, w, (hipStream_t)stream);
 }

@@ -393,6 +393,25 @@ int aima_moe_stack_decode_routed(const aima_moe_layer* layers,
                                  uint16_t* out, void* workspace,
                                  size_t workspace_bytes, void* stream);
 
+/* aima_moe_stack_decode_routed without a workspace and without any
+ * allocation: the scratch (normalized input, residual ping-pong, router
+ * logits, activations) is a fixed 128 KiB device array inside this library,
+ * one per GPU, held until the process ends.  No counterpart in the reference:
+ * it is for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Device-detected errors
+ * are OR-ed into the caller's device word *error_word (never cleared here).
+ * The scratch takes (k + 1) * inter * 2 + 3 * hidden * 2 + 4.6 KiB: at most
+ * 97 KiB for every shape the decode kernels accept (hidden <= 4096,
+ * inter <= 2048, k <= 16); a shape past 128 KiB would return
+ * AIMA_E_UNSUPPORTED.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (other streams, other threads)
+ * race and must be serialized by the caller. */
+int aima_moe_stack_decode_routed_noalloc(const aima_moe_layer* layers,
+                                         const aima_u4_tensor* routers, int32_t n_layers,
+                                         float eps, const uint16_t* residual_in, int32_t k,
+                                         float min_weight_sum, int32_t* ids, float* weights,
+                                         uint16_t* out, uint32_t* error_word, void* stream);
+
 /* Resident decode plan: the whole n_layers-layer decode step in ONE
  * persistent launch (hidden 2048, inter 512, k <= 8; see
  * moe_decode_persistent.hip).  create() validates the shapes, checks that
