@@ -318,10 +318,13 @@ def q4k_scale_min(packed12, j: int):
     return (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4), (q[j + 4] >> 4) | ((q[j] >> 6) << 4)
 
 
-def q4k_unpack(raw, rows: int, cols: int):
+def q4k_unpack(raw, rows: int, cols: int, f32_scale: bool = False):
     """Q4_K [rows][cols] -> (codes u8 [rows][cols/2] boundary packing, scale
     f16 bits [rows][cols/32] = f16(d * sc), min f32 [rows][cols/32] = dmin * m)
-    (tools/intel-qwen36-openvino-moe-micro-prepack.py:91-124; row-major)."""
+    (tools/intel-qwen36-openvino-moe-micro-prepack.py:91-124; row-major).
+    With f32_scale, a fourth output: the f32 scale d * sc before the f16
+    rounding (the d1 / d2 of the reference's decode_q4_k_block,
+    gguf_loader.cpp:1011-1040)."""
     bpr = cols // Q4K_VALUES
     b = np.asarray(raw, np.uint8).reshape(rows, bpr, Q4K_BYTES)
     codes = np.empty((rows, cols), np.uint8)
@@ -344,6 +347,8 @@ def q4k_unpack(raw, rows: int, cols: int):
                 mn[r, blk, j] = np.float32(dmin[r, blk]) * np.float32(m6)
     packed = (codes[:, 0::2] | (codes[:, 1::2] << 4)).astype(np.uint8)
     scale = sc.reshape(rows, bpr * 8).astype(np.float16).view(np.uint16)
+    if f32_scale:
+        return packed, scale, mn.reshape(rows, bpr * 8), sc.reshape(rows, bpr * 8)
     return packed, scale, mn.reshape(rows, bpr * 8)
 
 
@@ -561,6 +566,7 @@ class Ref:
         L.ref_matvec_f32.argtypes = [C.c_char_p, _f32p, _i64, _i64, _f32p, _f32p]
         L.ref_moe_ffn_layer_f32.argtypes = [C.c_char_p, _i64, _i64, _i64, _i64] + \
             [_f32p] * 8 + [C.c_float] + [C.c_void_p] * 12
+        L.ref_decode_q4k_rows.argtypes = [C.c_char_p, _u8p, _i64, _i64, _f32p]
         self.L = L
 
     def _check(self, rc, what):
@@ -569,6 +575,15 @@ class Ref:
 
     def sigmoid_scalar(self, v):
         return float(self.L.ref_sigmoid_scalar(v))
+
+    def decode_q4k_rows(self, raw, rows: int, cols: int, path: str):
+        """The reference's Q4_K decode (decode_q4_k_block via decode_tensor_row)
+        of a raw [rows][cols] tensor -> f32 [rows][cols]."""
+        raw = np.ascontiguousarray(raw, np.uint8).reshape(-1)
+        out = np.empty((rows, cols), np.float32)
+        self._check(self.L.ref_decode_q4k_rows(path.encode(), raw, rows, cols, out),
+                    "decode_q4k_rows")
+        return out
 
     def softmax(self, logits):
         logits = _f32(logits).reshape(-1)

@@ -37,11 +37,20 @@ void copy_out(const std::vector<float>& v, float* out) {
   if (out) std::memcpy(out, v.data(), v.size() * sizeof(float));
 }
 
+// One GGUF tensor: dims innermost first, ggml type (0 = F32, 12 = Q4_K) and
+// its raw payload.
 struct F32Tensor {
   std::string name;
   std::vector<std::uint64_t> dims;
   const float* data;
   std::uint64_t count;
+  std::uint32_t type = 0;
+  const void* raw = nullptr;   // payload for non-F32 types
+  std::uint64_t raw_bytes = 0;
+  std::uint64_t nbytes() const { return type == 0 ? count * 4 : raw_bytes; }
+  const char* bytes() const {
+    return type == 0 ? reinterpret_cast<const char*>(data) : static_cast<const char*>(raw);
+  }
 };
 
 void put_u32(std::ofstream& out, std::uint32_t v) {
@@ -76,17 +85,16 @@ void write_gguf_f32(const std::string& path,
     put_str(out, t.name);
     put_u32(out, static_cast<std::uint32_t>(t.dims.size()));
     for (auto d : t.dims) put_u64(out, d);
-    put_u32(out, 0);               // GGML_TYPE_F32
+    put_u32(out, t.type);          // ggml type
     put_u64(out, offset);
     offsets.push_back(offset);
-    offset += (t.count * 4 + kAlign - 1) / kAlign * kAlign;
+    offset += (t.nbytes() + kAlign - 1) / kAlign * kAlign;
   }
   auto pos = static_cast<std::uint64_t>(out.tellp());
   for (; pos % kAlign != 0; ++pos) out.put('\0');
   for (const auto& t : tensors) {
-    out.write(reinterpret_cast<const char*>(t.data),
-              static_cast<std::streamsize>(t.count * 4));
-    for (std::uint64_t b = t.count * 4; b % kAlign != 0; ++b) out.put('\0');
+    out.write(t.bytes(), static_cast<std::streamsize>(t.nbytes()));
+    for (std::uint64_t b = t.nbytes(); b % kAlign != 0; ++b) out.put('\0');
   }
   if (!out) throw std::runtime_error("GGUF write failed");
 }
@@ -263,6 +271,34 @@ int ref_moe_ffn_layer_f32(const char* path, std::int64_t H, std::int64_t I,
     copy_out(r.shared_down, shared_down);
     copy_out(r.ffn_out, ffn_out);
     copy_out(r.residual, residual_out);
+    return 0;
+  } catch (const std::exception& e) {
+    std::remove(path);
+    return fail(e);
+  }
+}
+
+// Q4_K rows decoded by the reference: a GGUF file with one Q4_K tensor
+// [rows][cols] (raw 144-byte super-blocks, row-major) read back row by row
+// through decode_tensor_row (gguf_loader.cpp:3245), which decodes each block
+// with decode_q4_k_block (gguf_loader.cpp:1011-1040).
+int ref_decode_q4k_rows(const char* path, const std::uint8_t* blocks, std::int64_t rows,
+                        std::int64_t cols, float* out) {
+  try {
+    F32Tensor t{"blk.0.ffn_down_exps.weight",
+                {static_cast<std::uint64_t>(cols), static_cast<std::uint64_t>(rows)},
+                nullptr, static_cast<std::uint64_t>(rows * cols)};
+    t.type = 12;
+    t.raw = blocks;
+    t.raw_bytes = static_cast<std::uint64_t>(rows * (cols / 256) * 144);
+    write_gguf_f32(path, {t});
+    auto index = iq36::parse_gguf_model_index(path);
+    for (std::int64_t r = 0; r < rows; ++r) {
+      const auto v = iq36::decode_tensor_row(path, index, t.name, static_cast<std::uint64_t>(r));
+      if (static_cast<std::int64_t>(v.size()) != cols) throw std::runtime_error("row size");
+      std::memcpy(out + r * cols, v.data(), sizeof(float) * static_cast<std::size_t>(cols));
+    }
+    std::remove(path);
     return 0;
   } catch (const std::exception& e) {
     std::remove(path);

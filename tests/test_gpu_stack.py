@@ -82,16 +82,18 @@ def test_small_stack_decode_and_prefill(pkg, dev):
     ids_np, w_np = ids.cpu().numpy(), w.cpu().numpy()
     # teacher-forced: every GPU layer starts from the oracle's input (2e-3 bar)
     r = f16_bits(x)
+    eps = []
     for L in range(len(layers)):
         nxt = oracle_stack([lnp[L]], [norms[L]], r, ids_np[L:L + 1], w_np[L:L + 1])
         got = pkg.moe_stack_prefill([layers[L]], torch.from_numpy(r.view(np.float16)).to(dev),
                                     ids[L:L + 1].contiguous(), w[L:L + 1].contiguous(),
                                     epsilon=EPS)
         torch.cuda.synchronize()
-        assert_parity(f16_to_f32(got), oracle.f16_values(nxt), what=f"small stack prefill layer {L}")
+        eps.append(assert_parity(f16_to_f32(got), oracle.f16_values(nxt),
+                                 what=f"small stack prefill layer {L}")["max_rel"])
         r = nxt
     # free-running: f16 rounding differences carried through the residual
-    assert_parity(f16_to_f32(out), oracle.f16_values(r), tol=PREFILL_END_TO_END_TOL,
+    assert_parity(f16_to_f32(out), oracle.f16_values(r), tol=end_to_end_bound(eps),
                   what="small stack prefill end-to-end")
 
 
@@ -128,18 +130,22 @@ def _oracle_layer(layer, r_bits, ids_np, w_np):
     return oracle.float_to_half(o).reshape(o.shape)
 
 
-# After 40 layers the f16 residual stream (|r| ~ 1e3, f16 ulp 0.5-1) carries
-# rounding differences that compound like a random walk: wherever GPU and
-# oracle FFN outputs (which agree to ~1e-4) straddle an f16 rounding point,
-# the residual differs by one ulp and the difference propagates.  Per-layer
-# parity is therefore checked teacher-forced at the 2e-3 bar (every GPU layer
-# starts from the oracle's own input), and the free-running 40-layer result
-# is held to max |diff| / max |ref| <= 1e-2 (decode) and cosine >= 0.9999.
-# The prefill GEMM also rounds each dequantized weight (q - z) * s to f16
-# (relative 2^-11; a bf16 tile would round to 2^-9), which adds a per-layer
-# perturbation of the same order; its free-running bound is 2e-2.
-END_TO_END_TOL = 1e-2
-PREFILL_END_TO_END_TOL = 2e-2
+# End-to-end bound, derived from the measured per-layer errors.  Every layer
+# is first checked teacher-forced at the 2e-3 bar: GPU and oracle start from
+# the same input, and eps_L = max |diff| / max |ref| of that layer's output.
+# Free-running, the f16 residual stream r_{L+1} = f16(r_L + ffn_L) carries
+# each layer's discrepancy forward almost unamplified (d ffn / d r is small:
+# the FFN output is a fraction of |r| and RMSNorm removes the scale), and
+# the per-layer discrepancies are independent rounding noise, so after L
+# layers the max-norm difference behaves like a random walk,
+#   max |diff_L| / max |ref_L|  ~  sqrt(sum_l eps_l^2),
+# (eps_l is already a max over the 2048 outputs).  f16 rounding flips are
+# part of eps_l: where GPU and oracle straddle a rounding point they differ
+# by one ulp, which is what eps_l measures.  The tests assert the free-running
+# result against 3 * sqrt(sum eps_l^2) -- the random walk plus a factor 3 for
+# its spread -- with the measured eps_l, not a fixed number.
+def end_to_end_bound(eps):
+    return 3.0 * float(np.sqrt(np.sum(np.square(eps))))
 
 
 def test_config4a_decode_40_layers(pkg, dev, stack40):
@@ -149,41 +155,77 @@ def test_config4a_decode_40_layers(pkg, dev, stack40):
     torch.cuda.synchronize()
     ids_np, w_np = ids.cpu().numpy(), w.cpu().numpy()
     r = f16_bits(x)
+    eps = []
     for L, layer in enumerate(stack40):
         nxt = _oracle_layer(layer, r, ids_np[L], w_np[L])
         got = pkg.moe_stack_decode([layer], torch.from_numpy(r[0].view(np.float16)).to(dev),
                                    ids[L].contiguous(), w[L].contiguous(), EPS)
         torch.cuda.synchronize()
-        assert_parity(f16_to_f32(got), oracle.f16_values(nxt[0]), what=f"config4a layer {L}")
+        eps.append(assert_parity(f16_to_f32(got), oracle.f16_values(nxt[0]),
+                                 what=f"config4a layer {L}")["max_rel"])
         r = nxt
-    c = assert_parity(f16_to_f32(out), oracle.f16_values(r[0]), tol=END_TO_END_TOL,
-                      what="config4a end-to-end")
+    bound = end_to_end_bound(eps)
+    c = assert_parity(f16_to_f32(out), oracle.f16_values(r[0]), tol=bound,
+                      what=f"config4a end-to-end (bound {bound:.2e})")
     assert c["cosine"] >= 0.9999
 
 
-def test_config4b_prefill_40_layers_sampled(pkg, dev, stack40):
+def test_config4b_prefill_40_layers_full_tiles(pkg, dev, stack40):
+    """Config 4b, T = 16384 (full 256-row tiles, every expert ~512 rows).
+    Layer by layer at the full T: each GPU layer runs on the GPU's own input
+    for all tokens, and the oracle runs the same layer on the same input rows
+    for sampled tokens (teacher-forced per layer at the 2e-3 bar).  The
+    40-layer stack (fused combine: next layer's RMSNorm and shared gate in
+    the combine kernel) equals the layer-by-layer runs bit for bit, and the
+    sampled tokens' free-running oracle chain bounds the end-to-end result."""
     T = 16384
     x = pkg.synth.activations(T, 2048, 43, dev)
     ids, w = routing(pkg, dev, 40, T, 256, 44)
     out = pkg.moe_stack_prefill(stack40, x, ids, w, EPS)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
-    sel = np.array([0, 1, 5000, 16383])
+    sel = np.array([0, 1, 777, 5000, 8191, 12345, 16000, 16383])
     ids_np = ids.cpu().numpy()[:, sel]
     w_np = w.cpu().numpy()[:, sel]
-    r = f16_bits(x)[sel]
+    r = x
+    eps = []
     for L, layer in enumerate(stack40):
-        nxt = _oracle_layer(layer, r, ids_np[L], w_np[L])
-        # the same layer on the GPU grouped path for the sampled tokens (T = 4)
-        got = pkg.moe_stack_prefill([layer], torch.from_numpy(r.view(np.float16)).to(dev),
-                                    torch.from_numpy(ids_np[L:L + 1]).to(dev),
-                                    torch.from_numpy(w_np[L:L + 1]).to(dev), EPS)
+        nxt = pkg.moe_stack_prefill([layer], r, ids[L:L + 1].contiguous(),
+                                    w[L:L + 1].contiguous(), EPS)
         torch.cuda.synchronize()
-        assert_parity(f16_to_f32(got), oracle.f16_values(nxt), what=f"config4b layer {L}")
+        ref = _oracle_layer(layer, f16_bits(r)[sel], ids_np[L], w_np[L])
+        eps.append(assert_parity(f16_to_f32(nxt)[sel], oracle.f16_values(ref),
+                                 what=f"config4b layer {L} (T=16384)")["max_rel"])
         r = nxt
-    c = assert_parity(f16_to_f32(out)[sel], oracle.f16_values(r), tol=PREFILL_END_TO_END_TOL,
-                      what="config4b end-to-end")
+    assert torch.equal(r, out), "fused 40-layer stack differs from the layer-by-layer runs"
+    chain = f16_bits(x)[sel]
+    for L, layer in enumerate(stack40):
+        chain = _oracle_layer(layer, chain, ids_np[L], w_np[L])
+    bound = end_to_end_bound(eps)
+    c = assert_parity(f16_to_f32(out)[sel], oracle.f16_values(chain), tol=bound,
+                      what=f"config4b end-to-end (bound {bound:.2e})")
     assert c["cosine"] >= 0.9999
+
+
+def test_stack_prefill_fused_combine_three_layers(pkg, dev):
+    """H = 2048 stacks fuse the next layer's RMSNorm and shared gate into the
+    combine kernel: a 3-layer stack equals three 1-layer stacks bit for bit,
+    and layers 1 and 2 match the oracle teacher-forced on every token."""
+    layers = make_stack(pkg, dev, 3, 2048, 512, 32, seed=1500)
+    T = 200
+    x = pkg.synth.activations(T, 2048, 1501, dev)
+    ids, w = routing(pkg, dev, 3, T, 32, 1502)
+    out = pkg.moe_stack_prefill(layers, x, ids, w, EPS)
+    r = x
+    for L in range(3):
+        nxt = pkg.moe_stack_prefill([layers[L]], r, ids[L:L + 1].contiguous(),
+                                    w[L:L + 1].contiguous(), EPS)
+        torch.cuda.synchronize()
+        if L > 0:
+            ref = _oracle_layer(layers[L], f16_bits(r), ids.cpu().numpy()[L], w.cpu().numpy()[L])
+            assert_parity(f16_to_f32(nxt), oracle.f16_values(ref), what=f"fused stack layer {L}")
+        r = nxt
+    assert torch.equal(out, r)
 
 
 # ---------------------------------------------------------------------------
@@ -306,17 +348,20 @@ def test_config4a_decode_plan_40_layers(pkg, dev, stack40):
     assert plan.error_bits() == 0
     ids_np, w_np = ids.cpu().numpy(), w.cpu().numpy()
     r = f16_bits(x)
+    eps = []
     for L, layer in enumerate(stack40):
         nxt = _oracle_layer(layer, r, ids_np[L:L + 1], w_np[L:L + 1])
         one = pkg.DecodePlan([layer], k=8)
         got = one.run(torch.from_numpy(r[0].view(np.float16)).to(dev), ids=ids[L:L + 1],
                       weights=w[L:L + 1])
         torch.cuda.synchronize()
-        assert_parity(f16_to_f32(got), oracle.f16_values(nxt[0]), what=f"plan layer {L}")
+        eps.append(assert_parity(f16_to_f32(got), oracle.f16_values(nxt[0]),
+                                 what=f"plan layer {L}")["max_rel"])
         one.close()
         r = nxt
-    c = assert_parity(f16_to_f32(out), oracle.f16_values(r[0]), tol=END_TO_END_TOL,
-                      what="plan 40-layer end-to-end")
+    bound = end_to_end_bound(eps)
+    c = assert_parity(f16_to_f32(out), oracle.f16_values(r[0]), tol=bound,
+                      what=f"plan 40-layer end-to-end (bound {bound:.2e})")
     assert c["cosine"] >= 0.9999
 
 

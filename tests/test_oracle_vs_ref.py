@@ -109,3 +109,27 @@ def test_moe_ffn_layer_bit_exact(ref, tmp_path, seed):
     t = oracle.moe_ffn_tokens(mw, r["ffn_norm"][None], r["ids"][None],
                               r["normalized_weights"][None], residual=residual[None])
     assert bits_equal(t[0], r["residual"])
+
+
+def test_q4k_unpack_matches_reference_decode(ref, tmp_path):
+    """oracle.q4k_unpack against the reference's own decode_q4_k_block (through
+    decode_tensor_row on a GGUF Q4_K tensor): its codes, f32 scales and mins
+    rebuild every reference value exactly as d1 * q - m1, and its f16 scales
+    are those f32 scales rounded to nearest even.  Random blocks, including
+    f16 subnormal and large d / dmin and every 6-bit scale / min."""
+    rng = np.random.default_rng(12)
+    rows, cols = 24, 512
+    raw = rng.integers(0, 256, (rows, cols // 256, 144), dtype=np.uint8)
+    d = np.concatenate([rng.uniform(-2, 2, rows * 2 - 6), [6e-8, -6e-8, 3e-5, 1e-3, 60000.0, 0.0]])
+    dm = rng.uniform(-0.5, 0.5, rows * 2)
+    raw[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(rows, 2, 2)
+    raw[:, :, 2:4] = dm.astype(np.float16).view(np.uint8).reshape(rows, 2, 2)
+    vals = ref.decode_q4k_rows(raw, rows, cols, str(tmp_path / "q4k.gguf"))
+    codes, s16, mins, s32 = oracle.q4k_unpack(raw, rows, cols, f32_scale=True)
+    q = np.empty((rows, cols), np.float32)
+    q[:, 0::2] = codes & 15
+    q[:, 1::2] = codes >> 4
+    rebuilt = np.repeat(s32, 32, axis=1) * q - np.repeat(mins, 32, axis=1)
+    assert rebuilt.dtype == np.float32
+    assert np.array_equal(rebuilt.view(np.uint32), vals.view(np.uint32))
+    assert np.array_equal(s16, s32.astype(np.float16).view(np.uint16))
