@@ -66,29 +66,45 @@ struct RowGeom {
   static constexpr int K = KCH * 32;
 };
 
-// Load the lane's activation chunks (chunk c = cl + i*SEG) from f16 x.
+// The lane's activation chunks (chunk c = cl + i*SEG of f16 x) as raw
+// 16-byte words; make_xchunk builds the dot-product operands once they land.
 template <int KCH>
-__device__ __forceinline__ void load_x_chunks(const uint16_t* __restrict__ x,
-                                              int cl, XChunk (&xc)[RowGeom<KCH>::NC]) {
+__device__ __forceinline__ void load_x_raw(const uint16_t* __restrict__ x, int cl,
+                                           u32x4 (&xr)[RowGeom<KCH>::NC][4]) {
   using G = RowGeom<KCH>;
 #pragma unroll
   for (int i = 0; i < G::NC; ++i) {
-    const int c = cl + i * G::SEG;
-    const u32x4* p = reinterpret_cast<const u32x4*>(x + (int64_t)c * 32);
+    const u32x4* p = reinterpret_cast<const u32x4*>(x + (int64_t)(cl + i * G::SEG) * 32);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xr[i][q] = p[q];
+  }
+}
+
+template <int KCH>
+__device__ __forceinline__ void build_x_chunks(const u32x4 (&xr)[RowGeom<KCH>::NC][4],
+                                               XChunk (&xc)[RowGeom<KCH>::NC]) {
+  using G = RowGeom<KCH>;
+#pragma unroll
+  for (int i = 0; i < G::NC; ++i) {
     uint32_t w[16];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const u32x4 v = p[q];
-      w[4 * q + 0] = v[0];
-      w[4 * q + 1] = v[1];
-      w[4 * q + 2] = v[2];
-      w[4 * q + 3] = v[3];
+      w[4 * q + 0] = xr[i][q][0];
+      w[4 * q + 1] = xr[i][q][1];
+      w[4 * q + 2] = xr[i][q][2];
+      w[4 * q + 3] = xr[i][q][3];
     }
     make_xchunk(w, xc[i]);
   }
 }
 
 // Rows blk * BR .. +BR of one matrix (the body of every matvec block).
+//
+// Load order: the block's scales and zero points (contiguous: its rows are
+// consecutive), then the activations, then the weights, with nothing waited
+// for in between.  Loads complete in order, so staging the scales in LDS
+// and building the activation operands waits only for those, while every
+// weight load is still in flight.
 template <int KCH, int RG>
 __device__ __forceinline__ void matvec_block(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ qw,
@@ -97,13 +113,14 @@ __device__ __forceinline__ void matvec_block(
   using G = RowGeom<KCH>;
   constexpr int BR = 4 * RG * G::RPI;       // rows of the block (consecutive)
   constexpr int kMaxGroups = G::K / 32;     // groups per row at group 32
-  // The block's scales and zero points are contiguous: staged through LDS
-  // with one element per thread (a scale and a zero-point load per lane and
-  // row would cost two memory instructions per 16-byte weight load).
-  __shared__ uint16_t s_lds[BR * kMaxGroups];
-  __shared__ uint8_t z_lds[BR * kMaxGroups / 2];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // 32-bit words of scales / zero points per thread at the most groups
+  constexpr int kSW = (BR * kMaxGroups / 2 + 255) / 256;
+  constexpr int kZW = (BR * kMaxGroups / 8 + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t s_lds[BR * kMaxGroups];
+  __shared__ __attribute__((aligned(16))) uint8_t z_lds[BR * kMaxGroups / 2];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
   const int seg = lane / G::SEG;
   const int cl = lane % G::SEG;
   const int groups = G::K >> group_log2;
@@ -111,25 +128,56 @@ __device__ __forceinline__ void matvec_block(
 
   const int64_t brow0 = blk * BR;
   const int64_t row0 = brow0 + (int64_t)wave * (RG * G::RPI);
+  const int64_t rows_here = n - brow0 < BR ? n - brow0 : BR;
+  const int nsc = (int)rows_here * groups;  // scales (and zero-point nibbles) of the block
+  const int zbytes = (nsc + 1) / 2;
+  const uint16_t* sblk = scale + brow0 * groups;
+  const uint8_t* zblk = zp + (brow0 * groups >> 1);
+  // 32-bit words where the block's runs are 4-byte aligned (always, for
+  // 4-byte aligned arrays); the remainder element by element
+  const bool s_words = (reinterpret_cast<uintptr_t>(sblk) & 3u) == 0;
+  const bool z_words = (reinterpret_cast<uintptr_t>(zblk) & 3u) == 0;
+  const int s_full = s_words ? nsc / 2 : 0, z_full = z_words ? zbytes / 4 : 0;
+  uint32_t sw[kSW], zw[kZW];
+#pragma unroll
+  for (int j = 0; j < kSW; ++j) {
+    const int i = tid + 256 * j;
+    sw[j] = i < s_full ? reinterpret_cast<const uint32_t*>(sblk)[i] : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < kZW; ++j) {
+    const int i = tid + 256 * j;
+    zw[j] = i < z_full ? reinterpret_cast<const uint32_t*>(zblk)[i] : 0u;
+  }
+  u32x4 xr[G::NC][4];
+  load_x_raw<KCH>(x, cl, xr);
+  // rows past n load row n - 1 instead (straight-line loads, no branch
+  // around each); their results are never written
   u32x4 w[RG][G::NC];
 #pragma unroll
   for (int r = 0; r < RG; ++r) {
     const int64_t row = row0 + r * G::RPI + seg;
+    const int64_t rowc = row < n ? row : n - 1;
 #pragma unroll
     for (int i = 0; i < G::NC; ++i) {
       const int c = cl + i * G::SEG;
-      w[r][i] = row < n ? load16_nt(qw + row * (G::K / 2) + (int64_t)c * 16)
-                        : u32x4{0u, 0u, 0u, 0u};
+      w[r][i] = load16_nt(qw + rowc * (G::K / 2) + (int64_t)c * 16);
     }
   }
-  {
-    const int64_t rows_here = n - brow0 < BR ? n - brow0 : BR;
-    const int nsc = (int)rows_here * groups;  // scales (and zero-point nibbles) of the block
-    for (int t = threadIdx.x; t < nsc; t += 256) s_lds[t] = scale[brow0 * groups + t];
-    for (int t = threadIdx.x; t < (nsc + 1) / 2; t += 256) z_lds[t] = zp[(brow0 * groups >> 1) + t];
+#pragma unroll
+  for (int j = 0; j < kSW; ++j) {
+    const int i = tid + 256 * j;
+    if (i < s_full) reinterpret_cast<uint32_t*>(s_lds)[i] = sw[j];
   }
+#pragma unroll
+  for (int j = 0; j < kZW; ++j) {
+    const int i = tid + 256 * j;
+    if (i < z_full) reinterpret_cast<uint32_t*>(z_lds)[i] = zw[j];
+  }
+  for (int t = 2 * s_full + tid; t < nsc; t += 256) s_lds[t] = sblk[t];
+  for (int t = 4 * z_full + tid; t < zbytes; t += 256) z_lds[t] = zblk[t];
   XChunk xc[G::NC];
-  load_x_chunks<KCH>(x, cl, xc);
+  build_x_chunks<KCH>(xr, xc);
   __syncthreads();
 #pragma unroll
   for (int r = 0; r < RG; ++r) {

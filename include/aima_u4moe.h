@@ -207,16 +207,21 @@ int aima_topk_workspace_size(int64_t n, int32_t k, size_t* bytes);
 /* Top-k of n f32 values (an LM head's logits): ids[r], values[r] for ranks
  * r < k, value descending, the lower index first among equal values (the
  * order of the reference's LM-head partial top-8, q4x8_matvec.cl:973-1021).
- * n <= 1,048,576, k <= 16; the workspace may be null when n <= 1024. */
+ * NaNs are never chosen; ranks past the last number hold (-inf, 0x7fffffff).
+ * n <= 1,048,576, k <= 16; the workspace may be null when n <= 1024.  One
+ * launch: its blocks meet at a counter in the workspace header (bytes
+ * 128..135), which must be zero when the workspace is first used (as the
+ * error word must be) and which every call leaves zero; calls sharing a
+ * workspace must not overlap. */
 int aima_topk_f32(const float* values, int64_t n, int32_t k, int32_t* ids,
                   float* out_values, void* workspace, size_t workspace_bytes,
                   void* stream);
 
 /* U4 LM head with top-k: logits = f32 U4 matvec of x (as aima_u4_matvec,
  * kept in the caller's logits buffer of n floats), then aima_topk_f32 over
- * them.  Replaces the reference's q4s_group128_lm_head_topk8_f32
- * (engine/gpu/opencl/q4x8_matvec.cl:973-1021: logits out plus per-block
- * partial top-8 ids and values) with its merge. */
+ * them (same workspace rules).  Replaces the reference's
+ * q4s_group128_lm_head_topk8_f32 (engine/gpu/opencl/q4x8_matvec.cl:973-1021:
+ * logits out plus per-block partial top-8 ids and values) with its merge. */
 int aima_u4_lm_head_topk(const uint16_t* x, const uint8_t* qweight,
                          const uint16_t* scale, const uint8_t* zp, int64_t n,
                          int64_t k, int32_t group, int32_t topk, float* logits,

@@ -54,7 +54,7 @@ def test_topk_distinct_and_infinite(pkg, dev):
     assert np.array_equal(ids.cpu().numpy(), ref_i) and np.array_equal(vals.cpu().numpy(), ref_v)
 
 
-@pytest.mark.parametrize("k", [1, 8])
+@pytest.mark.parametrize("k", [1, 8, 16])
 def test_lm_head_topk_config3(pkg, dev, k):
     """K=2048, N=248320: logits are the matvec's bit for bit, the selection is
     the oracle's on them, and the logits match the oracle's matvec."""
@@ -80,3 +80,109 @@ def test_topk_rejects_bad_sizes(pkg, dev):
         pkg.topk_f32(v, 17)
     with pytest.raises(pkg.AimaError):
         pkg.topk_f32(torch.zeros(1048577, device=dev), 8)
+
+
+# ---------------------------------------------------------------------------
+# fused LM-head top-k: the matvec blocks append candidates at or above a
+# shared threshold, one merge block selects (the state lives in the
+# workspace header and is cleared by every call)
+# ---------------------------------------------------------------------------
+
+def _structured_head(pkg, dev, n, K, scales, group=128):
+    """U4 head whose logits are 15 * s_row * sum(x) (q = 15, z = 0 everywhere,
+    one f16 scale per row repeated over its groups), so their order and ties
+    follow `scales`."""
+    G = K // group
+    q = torch.full((n, K // 2), 0xFF, dtype=torch.uint8, device=dev)
+    zp = torch.zeros(((n * G + 1) // 2,), dtype=torch.uint8, device=dev)
+    sc = scales.to(torch.float16).reshape(n, 1).expand(n, G).contiguous().to(dev)
+    return pkg.U4Weight(q, sc, zp, n, K, group)
+
+
+def _check_head(pkg, dev, w, x, k, ws=None):
+    ids, vals, logits = pkg.lm_head_topk(x, w, k, ws=ws)
+    single = pkg.matvec_u4(x, w, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    # the fused matvec's logits are the plain matvec's bit for bit (NaN too)
+    assert torch.equal(logits.view(torch.int32), single.view(torch.int32))
+    ref_i, ref_v = oracle.lm_head_topk(logits.cpu().numpy(), k)
+    assert np.array_equal(ids.cpu().numpy(), ref_i), (ids.cpu().numpy(), ref_i)
+    assert np.array_equal(vals.cpu().numpy(), ref_v)
+    return ids, vals
+
+
+@pytest.mark.parametrize("order", ["rising", "falling", "flat"])
+@pytest.mark.parametrize("k", [1, 8, 16])
+def test_lm_head_topk_ordered_and_tied(pkg, dev, order, k):
+    """Rising logits make every block beat the threshold of the blocks before
+    it (the longest candidate list: k per block, merged in many chunks);
+    falling ones stop the list after the first blocks; flat ones tie every
+    row (lowest indices win).  f16 scales repeat, so ties occur throughout."""
+    n, K = 100_000, 2048
+    ramp = torch.linspace(0.01, 2.0, n)
+    scales = {"rising": ramp, "falling": ramp.flip(0), "flat": torch.full((n,), 0.5)}[order]
+    w = _structured_head(pkg, dev, n, K, scales)
+    x = torch.full((K,), 0.25, dtype=torch.float16, device=dev)
+    ids, _ = _check_head(pkg, dev, w, x, k)
+    if order == "flat":
+        assert ids.cpu().tolist() == list(range(k))
+
+
+@pytest.mark.parametrize("K", [128, 512, 8192])
+@pytest.mark.parametrize("n,k", [(5, 5), (700, 16), (33333, 8)])
+def test_lm_head_topk_shapes(pkg, dev, K, n, k):
+    """Every block geometry (512 rows per block at K = 128 down to 16 at
+    K = 8192), partial last blocks and n = k."""
+    gen = pkg.synth.generator(K + n + k, dev)
+    w = pkg.synth.u4_weight(1, n, K, 128, gen, dev)
+    x = pkg.synth.activations(1, K, K + n, dev)[0]
+    _check_head(pkg, dev, w, x, k)
+
+
+def test_lm_head_topk_nan_and_infinite_rows(pkg, dev):
+    """NaN logits are never chosen (with at least k numbers present); +inf
+    rows lead; -inf rows rank after every finite value."""
+    n, K = 50_000, 2048
+    scales = torch.linspace(0.01, 1.0, n)
+    scales[7::97] = float("nan")
+    scales[40_000] = float("inf")
+    scales[123] = float("inf")
+    w = _structured_head(pkg, dev, n, K, scales)
+    x = torch.full((K,), 0.25, dtype=torch.float16, device=dev)
+    ids, vals = _check_head(pkg, dev, w, x, 8)
+    assert ids[0].item() == 123 and ids[1].item() == 40_000
+    xn = -x  # all logits negative: -inf rows now rank last
+    _check_head(pkg, dev, w, xn, 16)
+
+
+def test_lm_head_topk_zero_logits_tie(pkg, dev):
+    """Zero logits (rows with a zero scale, of either sign: the matvec's sums
+    start at +0, so a -0 scale still gives +0) under negative ones: the 24
+    zero rows tie and the lowest indices win, across blocks far apart."""
+    n, K = 40_000, 2048
+    scales = torch.full((n,), -1.0)
+    scales[30_000:30_020] = 0.0
+    scales[9_000:9_004] = -0.0
+    w = _structured_head(pkg, dev, n, K, scales)
+    x = torch.full((K,), 0.25, dtype=torch.float16, device=dev)
+    ids, vals = _check_head(pkg, dev, w, x, 8)
+    assert ids.cpu().tolist() == [9_000, 9_001, 9_002, 9_003, 30_000, 30_001, 30_002, 30_003]
+    assert (vals == 0).all()
+
+
+def test_lm_head_topk_state_cleared_between_calls(pkg, dev):
+    """The selection state in the workspace header is left zero by every
+    call: back-to-back calls with different inputs, a different k, and other
+    entry points using the same workspace in between all select exactly."""
+    ws = pkg.Workspace(dev)
+    gen = pkg.synth.generator(11, dev)
+    w = pkg.synth.u4_weight(1, 248320, 2048, 128, gen, dev)
+    for seed, k in ((1, 8), (2, 8), (3, 16), (4, 1)):
+        x = pkg.synth.activations(1, 2048, seed, dev)[0]
+        _check_head(pkg, dev, w, x, k, ws=ws)
+        v = torch.randn(300000, device=dev)
+        ids, vals = pkg.topk_f32(v, 8, ws=ws)
+        torch.cuda.synchronize()
+        ref_i, _ = oracle.lm_head_topk(v.cpu().numpy(), 8)
+        assert np.array_equal(ids.cpu().numpy(), ref_i)
+    assert ws.error_bits() == 0
