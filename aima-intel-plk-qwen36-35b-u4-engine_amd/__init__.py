@@ -13,9 +13,12 @@ from .layout import MoeLayerWeights, U4Weight  # noqa: F401
 from .ops import (  # noqa: F401
     MIN_WEIGHT_SUM,
     DecodePlan,
+    Qwen36MoeFfnLayerResult,
+    RouterTopKSelection,
     Workspace,
     apply_rms_norm,
     build_grouped_schedule,
+    ffn_layer_trace,
     grouped_moe_prefill,
     grouped_moe_prefill_routed,
     lm_head_topk,

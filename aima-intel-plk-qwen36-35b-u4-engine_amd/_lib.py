@@ -62,6 +62,14 @@ class PrefillViewsC(C.Structure):
                 ("tiles", _vp), ("tile_count", _vp)]
 
 
+class FfnTraceC(C.Structure):
+    _fields_ = [(name, _vp) for name in (
+        "ffn_norm", "router_logits", "expert_ids", "router_weights", "normalized_weights",
+        "selected_gate_up", "selected_swiglu", "selected_down", "weighted_selected_down",
+        "moe_out", "shared_gate", "shared_gate_sigmoid", "shared_gate_up", "shared_swiglu",
+        "shared_down", "shared_gated", "ffn_out", "residual")]
+
+
 _LP = C.POINTER(MoeLayerC)
 
 SIGNATURES = {
@@ -86,6 +94,9 @@ SIGNATURES = {
     "aima_moe_decode_workspace_size": (C.c_int, [_LP, _i32, _szp]),
     "aima_moe_ffn_decode": (C.c_int, [_LP, _vp, _vp, _vp, _vp, _i32, _vp, _vp, C.c_size_t,
                                       _vp]),
+    "aima_moe_ffn_layer_trace_workspace_size": (C.c_int, [_LP, _i32, _szp]),
+    "aima_moe_ffn_layer_trace": (C.c_int, [_LP, C.POINTER(U4TensorC), _vp, _f32, _i32, _f32,
+                                           C.POINTER(FfnTraceC), _vp, C.c_size_t, _vp]),
     "aima_moe_decode_gate_up": (C.c_int, [_LP, _vp, _vp, _i32, _vp, _vp, _vp, _vp]),
     "aima_moe_decode_down": (C.c_int, [_LP, _vp, _vp, _vp, _vp, _i32, _vp, _vp, _vp]),
     "aima_moe_prefill_workspace_size": (C.c_int, [_LP, _i64, _i32, _szp]),

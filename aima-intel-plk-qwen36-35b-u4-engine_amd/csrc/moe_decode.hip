@@ -103,7 +103,7 @@ template <int KCH>
 __global__ __launch_bounds__(256) void decode_gateup_kernel(
     const uint16_t* __restrict__ x, aima_moe_layer L, const int32_t* __restrict__ ids,
     int k, uint32_t* __restrict__ err, uint16_t* __restrict__ act,
-    float* __restrict__ sigma) {
+    float* __restrict__ sigma, float* __restrict__ gu_trace, float* __restrict__ gate_logit) {
   using G = Geom<KCH>;
   constexpr int NR = 2 * kPairsPerWave;          // rows per wave
   constexpr int PASSES = (NR + G::RPI - 1) / G::RPI;
@@ -221,6 +221,10 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
         }
       }
       act[pair] = f2h(silu_mul(g, u));
+      if (gu_trace) {  // the layer trace: gate and up rows, slot-major
+        gu_trace[slot * 2 * I + (pair - slot * I)] = g;
+        gu_trace[slot * 2 * I + I + (pair - slot * I)] = u;
+      }
     }
   }
   if (blockIdx.x == 0) {
@@ -229,6 +233,7 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
     if (threadIdx.x == 0) {
       const double r = t >= 0.0 ? 1.0 / (1.0 + exp(-t)) : exp(t) / (1.0 + exp(t));
       *sigma = (float)r;
+      if (gate_logit) *gate_logit = (float)t;
     }
   }
 }
@@ -236,11 +241,14 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
 // ---------------------------------------------------------------------------
 // phase B
 // ---------------------------------------------------------------------------
+// down_trace (the layer trace, else null): each slot's unweighted down row
+// sums, [(k+1)][H].
 template <int KCH>
 __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(
     aima_moe_layer L, const int32_t* __restrict__ ids, const float* __restrict__ rw, int k,
     const uint16_t* __restrict__ act, const float* __restrict__ sigma,
-    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out) {
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out,
+    float* __restrict__ down_trace) {
   using G = Geom<KCH>;
   constexpr int PASSES = (kDownRowsPerBlock + G::RPI - 1) / G::RPI;
   constexpr int NW = kDownThreads / 64;
@@ -319,6 +327,12 @@ __global__ __launch_bounds__(kDownThreads) void decode_down_kernel(
         for (int i = 0; i < G::NC; ++i)
           d += u4_chunk_dot(w[q][ps][i], xc[i], z[q][ps][i], s[q][ps][i], magic);
         acc[ps] += coef[q] * d;
+        if (down_trace) {
+          const float t = segment_sum<G::SEG>(d);
+          const int64_t row = h0 + ps * G::RPI + seg;
+          if (cl == 0 && ps * G::RPI + seg < kDownRowsPerBlock && row < H)
+            down_trace[(int64_t)slot * H + row] = t;
+        }
       }
     }
   }
@@ -374,46 +388,83 @@ static bool decode_shape_ok(const aima_moe_layer* L) {
          hk == 128) && (ik == 4 || ik == 8 || ik == 16 || ik == 32 || ik == 64);
 }
 
+// Trace buffers of aima_moe_ffn_layer_trace (all null on the product path).
+struct DecodeTrace {
+  float* gate_up;     // [(k+1)][2I]
+  float* gate_logit;  // [1]
+  float* down;        // [(k+1)][H]
+};
+
 template <int KCH>
 static void launch_gateup(const uint16_t* x, const aima_moe_layer& L, const int32_t* ids, int k,
-                          const DecodeWs& w, hipStream_t st) {
+                          const DecodeWs& w, const DecodeTrace& tr, hipStream_t st) {
   const int64_t pairs = (int64_t)(k + 1) * L.inter;
   const int64_t waves = (pairs + kPairsPerWave - 1) / kPairsPerWave;
   const int64_t blocks = (waves + 3) / 4;
   hipLaunchKernelGGL((decode_gateup_kernel<KCH>), dim3((unsigned)blocks), dim3(256), 0, st, x, L,
-                     ids, k, w.err, w.act, w.sigma);
+                     ids, k, w.err, w.act, w.sigma, tr.gate_up, tr.gate_logit);
 }
 
 template <int KCH>
 static void launch_down(const aima_moe_layer& L, const int32_t* ids, const float* rw, int k,
                         const DecodeWs& w, const uint16_t* residual, uint16_t* out,
-                        hipStream_t st) {
+                        const DecodeTrace& tr, hipStream_t st) {
   const int64_t blocks = (L.hidden + kDownRowsPerBlock - 1) / kDownRowsPerBlock;
   hipLaunchKernelGGL((decode_down_kernel<KCH>), dim3((unsigned)blocks), dim3(kDownThreads), 0, st, L,
-                     ids, rw, k, w.act, w.sigma, residual, out);
+                     ids, rw, k, w.act, w.sigma, residual, out, tr.down);
 }
 
 static int decode_layer(const aima_moe_layer& L, const uint16_t* x, const uint16_t* residual,
                         const int32_t* ids, const float* rw, int k, uint16_t* out,
-                        const DecodeWs& w, hipStream_t st) {
+                        const DecodeWs& w, hipStream_t st, const DecodeTrace& tr = DecodeTrace{}) {
   switch (L.hidden / 32) {
-    case 16: launch_gateup<16>(x, L, ids, k, w, st); break;
-    case 32: launch_gateup<32>(x, L, ids, k, w, st); break;
-    case 64: launch_gateup<64>(x, L, ids, k, w, st); break;
-    case 128: launch_gateup<128>(x, L, ids, k, w, st); break;
+    case 16: launch_gateup<16>(x, L, ids, k, w, tr, st); break;
+    case 32: launch_gateup<32>(x, L, ids, k, w, tr, st); break;
+    case 64: launch_gateup<64>(x, L, ids, k, w, tr, st); break;
+    case 128: launch_gateup<128>(x, L, ids, k, w, tr, st); break;
     default: return fail(AIMA_E_UNSUPPORTED, "moe decode: unsupported hidden size");
   }
   int rc = launch_check("moe decode gate/up");
   if (rc != AIMA_OK) return rc;
   switch (L.inter / 32) {
-    case 4: launch_down<4>(L, ids, rw, k, w, residual, out, st); break;
-    case 8: launch_down<8>(L, ids, rw, k, w, residual, out, st); break;
-    case 16: launch_down<16>(L, ids, rw, k, w, residual, out, st); break;
-    case 32: launch_down<32>(L, ids, rw, k, w, residual, out, st); break;
-    case 64: launch_down<64>(L, ids, rw, k, w, residual, out, st); break;
+    case 4: launch_down<4>(L, ids, rw, k, w, residual, out, tr, st); break;
+    case 8: launch_down<8>(L, ids, rw, k, w, residual, out, tr, st); break;
+    case 16: launch_down<16>(L, ids, rw, k, w, residual, out, tr, st); break;
+    case 32: launch_down<32>(L, ids, rw, k, w, residual, out, tr, st); break;
+    case 64: launch_down<64>(L, ids, rw, k, w, residual, out, tr, st); break;
     default: return fail(AIMA_E_UNSUPPORTED, "moe decode: unsupported intermediate size");
   }
   return launch_check("moe decode down");
+}
+
+// The layer trace's sums, one thread per output row: the weighted routed
+// rows and their rank-order sum (apply_expert_weights, aggregate_experts),
+// the gated shared row and the FFN output.  down: [(k+1)][H] unweighted.
+__global__ __launch_bounds__(256) void trace_combine_kernel(
+    const float* __restrict__ down, const float* __restrict__ rw, const float* __restrict__ sigma,
+    int k, int64_t H, float* __restrict__ weighted, float* __restrict__ moe_out,
+    float* __restrict__ shared_gated, float* __restrict__ ffn_out) {
+  // separately rounded products and sums (no contraction into fused
+  // multiply-adds), as the reference's separate passes compute them
+#pragma clang fp contract(off)
+  const int64_t h = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (h >= H) return;
+  float m = 0.f;
+  for (int r = 0; r < k; ++r) {
+    const float v = down[(int64_t)r * H + h] * rw[r];
+    weighted[(int64_t)r * H + h] = v;
+    m += v;
+  }
+  const float g = down[(int64_t)k * H + h] * *sigma;
+  moe_out[h] = m;
+  shared_gated[h] = g;
+  ffn_out[h] = m + g;
+}
+
+static size_t trace_ws_bytes(const aima_moe_layer& L, int k) {
+  return decode_ws_bytes(L.hidden, L.inter, k, false) +
+         round_up((size_t)(k + 1) * 2 * L.inter * 4, 256) +
+         round_up((size_t)(k + 1) * L.hidden * 4, 256);
 }
 
 int rmsnorm_launch(const uint16_t* x, const float* weight, int64_t rows, int64_t hidden,
@@ -422,7 +473,8 @@ int u4_matvec_dispatch(const uint16_t* x, const uint8_t* qw, const uint16_t* sca
                        const uint8_t* zp, int64_t n, int64_t k, int glog2, void* y,
                        int out_f32, hipStream_t st);
 int router_topk_launch(const float* logits, int64_t tokens, int experts, int k,
-                       float min_weight_sum, int32_t* ids, float* weights, hipStream_t st);
+                       float min_weight_sum, int32_t* ids, float* weights, hipStream_t st,
+                       float* probs = nullptr);
 int group_log2_of(int group);
 
 }  // namespace aima
@@ -435,6 +487,81 @@ extern "C" int aima_moe_decode_workspace_size(const aima_moe_layer* layer, int32
   AIMA_REQUIRE(k > 0, "moe_decode_workspace_size: k must be positive");
   *bytes = decode_ws_bytes(layer->hidden, layer->inter, k, true);
   return AIMA_OK;
+}
+
+extern "C" int aima_moe_ffn_layer_trace_workspace_size(const aima_moe_layer* layer, int32_t k,
+                                                       size_t* bytes) {
+  AIMA_REQUIRE(layer && bytes, "moe_ffn_layer_trace_workspace_size: null pointer");
+  AIMA_REQUIRE(k > 0, "moe_ffn_layer_trace_workspace_size: k must be positive");
+  *bytes = trace_ws_bytes(*layer, k);
+  return AIMA_OK;
+}
+
+extern "C" int aima_moe_ffn_layer_trace(const aima_moe_layer* layer, const aima_u4_tensor* router,
+                                        const uint16_t* residual, float eps, int32_t k,
+                                        float min_weight_sum, const aima_ffn_trace* t,
+                                        void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_layer(layer, k, true);
+  if (rc != AIMA_OK) return rc;
+  const aima_moe_layer& L = *layer;
+  AIMA_REQUIRE(router && router->qweight && router->scale && router->zp && residual && t,
+               "moe_ffn_layer_trace: null pointer");
+  AIMA_REQUIRE(t->ffn_norm && t->router_logits && t->expert_ids && t->router_weights &&
+                   t->normalized_weights && t->selected_gate_up && t->selected_swiglu &&
+                   t->selected_down && t->weighted_selected_down && t->moe_out &&
+                   t->shared_gate && t->shared_gate_sigmoid && t->shared_gate_up &&
+                   t->shared_swiglu && t->shared_down && t->shared_gated && t->ffn_out &&
+                   t->residual,
+               "moe_ffn_layer_trace: every trace buffer is required");
+  AIMA_REQUIRE(L.experts <= 1024 && k <= 16, "moe_ffn_layer_trace: experts <= 1024, k <= 16");
+  AIMA_REQUIRE(min_weight_sum > 0.f, "moe_ffn_layer_trace: minimum weight sum must be positive");
+  AIMA_REQUIRE(aligned(residual, 16) && aligned(t->ffn_norm, 16) && aligned(router->qweight, 16),
+               "moe_ffn_layer_trace: residual, ffn_norm and router qweight must be 16-byte "
+               "aligned");
+  if (!decode_shape_ok(layer)) {
+    return fail(AIMA_E_UNSUPPORTED, "moe_ffn_layer_trace: hidden/32 must be 16..128 and inter/32 4..64 (powers of two)");
+  }
+  if (!workspace || workspace_bytes < trace_ws_bytes(L, k)) {
+    return fail(AIMA_E_WORKSPACE, "moe_ffn_layer_trace: workspace missing or too small");
+  }
+  AIMA_REQUIRE(aligned(workspace, 256), "moe_ffn_layer_trace: workspace must be 256-byte aligned");
+  const hipStream_t st = (hipStream_t)stream;
+  const int64_t H = L.hidden, I = L.inter;
+  const DecodeWs w = decode_ws(workspace, H, I, k, false);
+  char* p = static_cast<char*>(workspace) + decode_ws_bytes(H, I, k, false);
+  DecodeTrace tr;
+  tr.gate_up = reinterpret_cast<float*>(p);
+  tr.down = reinterpret_cast<float*>(p + round_up((size_t)(k + 1) * 2 * I * 4, 256));
+  tr.gate_logit = t->shared_gate;
+  // ffn_norm, router logits and selection, then the decode kernels
+  rc = rmsnorm_launch(residual, L.norm_weight, 1, H, eps, t->ffn_norm, st);
+  if (rc != AIMA_OK) return rc;
+  rc = u4_matvec_dispatch(t->ffn_norm, router->qweight, router->scale, router->zp, L.experts, H,
+                          group_log2_of(L.group), t->router_logits, 1, st);
+  if (rc != AIMA_OK) return rc;
+  rc = router_topk_launch(t->router_logits, 1, L.experts, k, min_weight_sum, t->expert_ids,
+                          t->normalized_weights, st, t->router_weights);
+  if (rc != AIMA_OK) return rc;
+  rc = decode_layer(L, t->ffn_norm, residual, t->expert_ids, t->normalized_weights, k,
+                    t->residual, w, st, tr);
+  if (rc != AIMA_OK) return rc;
+  // the kernels' own intermediates, split into routed and shared parts
+  const size_t gu = (size_t)2 * I * 4, hf = (size_t)H * 4;
+  AIMA_HIP(hipMemcpyAsync(t->selected_gate_up, tr.gate_up, k * gu, hipMemcpyDeviceToDevice, st));
+  AIMA_HIP(hipMemcpyAsync(t->shared_gate_up, reinterpret_cast<char*>(tr.gate_up) + k * gu, gu,
+                          hipMemcpyDeviceToDevice, st));
+  AIMA_HIP(hipMemcpyAsync(t->selected_swiglu, w.act, (size_t)k * I * 2, hipMemcpyDeviceToDevice,
+                          st));
+  AIMA_HIP(hipMemcpyAsync(t->shared_swiglu, w.act + (size_t)k * I, (size_t)I * 2,
+                          hipMemcpyDeviceToDevice, st));
+  AIMA_HIP(hipMemcpyAsync(t->shared_gate_sigmoid, w.sigma, 4, hipMemcpyDeviceToDevice, st));
+  AIMA_HIP(hipMemcpyAsync(t->selected_down, tr.down, k * hf, hipMemcpyDeviceToDevice, st));
+  AIMA_HIP(hipMemcpyAsync(t->shared_down, reinterpret_cast<char*>(tr.down) + k * hf, hf,
+                          hipMemcpyDeviceToDevice, st));
+  hipLaunchKernelGGL(trace_combine_kernel, dim3((unsigned)((H + 255) / 256)), dim3(256), 0, st,
+                     tr.down, t->normalized_weights, w.sigma, k, H, t->weighted_selected_down,
+                     t->moe_out, t->shared_gated, t->ffn_out);
+  return launch_check("moe_ffn_layer_trace");
 }
 
 extern "C" int aima_moe_ffn_decode(const aima_moe_layer* layer, const uint16_t* x,
@@ -473,10 +600,10 @@ extern "C" int aima_moe_decode_gate_up(const aima_moe_layer* layer, const uint16
   w.sigma = shared_sigma;
   hipStream_t st = (hipStream_t)stream;
   switch (layer->hidden / 32) {
-    case 16: launch_gateup<16>(x, *layer, ids, k, w, st); break;
-    case 32: launch_gateup<32>(x, *layer, ids, k, w, st); break;
-    case 64: launch_gateup<64>(x, *layer, ids, k, w, st); break;
-    case 128: launch_gateup<128>(x, *layer, ids, k, w, st); break;
+    case 16: launch_gateup<16>(x, *layer, ids, k, w, DecodeTrace{}, st); break;
+    case 32: launch_gateup<32>(x, *layer, ids, k, w, DecodeTrace{}, st); break;
+    case 64: launch_gateup<64>(x, *layer, ids, k, w, DecodeTrace{}, st); break;
+    case 128: launch_gateup<128>(x, *layer, ids, k, w, DecodeTrace{}, st); break;
     default: return fail(AIMA_E_UNSUPPORTED, "moe decode: unsupported hidden size");
   }
   return launch_check("moe decode gate/up");
@@ -498,11 +625,11 @@ extern "C" int aima_moe_decode_down(const aima_moe_layer* layer, const uint16_t*
   w.sigma = const_cast<float*>(shared_sigma);
   hipStream_t st = (hipStream_t)stream;
   switch (layer->inter / 32) {
-    case 4: launch_down<4>(*layer, ids, weights, k, w, residual, out, st); break;
-    case 8: launch_down<8>(*layer, ids, weights, k, w, residual, out, st); break;
-    case 16: launch_down<16>(*layer, ids, weights, k, w, residual, out, st); break;
-    case 32: launch_down<32>(*layer, ids, weights, k, w, residual, out, st); break;
-    case 64: launch_down<64>(*layer, ids, weights, k, w, residual, out, st); break;
+    case 4: launch_down<4>(*layer, ids, weights, k, w, residual, out, DecodeTrace{}, st); break;
+    case 8: launch_down<8>(*layer, ids, weights, k, w, residual, out, DecodeTrace{}, st); break;
+    case 16: launch_down<16>(*layer, ids, weights, k, w, residual, out, DecodeTrace{}, st); break;
+    case 32: launch_down<32>(*layer, ids, weights, k, w, residual, out, DecodeTrace{}, st); break;
+    case 64: launch_down<64>(*layer, ids, weights, k, w, residual, out, DecodeTrace{}, st); break;
     default: return fail(AIMA_E_UNSUPPORTED, "moe decode: unsupported intermediate size");
   }
   return launch_check("moe decode down");

@@ -290,7 +290,8 @@ constexpr int kRouterMaxPerLane = 16;  // experts <= 1024
 template <int PER>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, int64_t tokens, int experts, int k,
-    float min_weight_sum, int32_t* __restrict__ ids, float* __restrict__ weights) {
+    float min_weight_sum, int32_t* __restrict__ ids, float* __restrict__ weights,
+    float* __restrict__ probs) {
   const int lane = threadIdx.x & 63;
   const int64_t token = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (token >= tokens) return;
@@ -350,35 +351,38 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   if (lane < k) {
     ids[token * k + lane] = my_i;
     weights[token * k + lane] = my_p / den;
+    if (probs) probs[token * k + lane] = my_p;  // the picks' softmax probabilities
   }
 }
 
 static void launch_router_topk(const float* logits, int64_t tokens, int experts, int k,
                                float min_weight_sum, int32_t* ids, float* weights,
-                               hipStream_t st) {
+                               hipStream_t st, float* probs = nullptr) {
   const unsigned blocks = (unsigned)((tokens + 3) / 4);
   const int per = (experts + 63) / 64;
   if (per <= 1) {
     hipLaunchKernelGGL(router_topk_kernel<1>, dim3(blocks), dim3(256), 0, st, logits, tokens,
-                       experts, k, min_weight_sum, ids, weights);
+                       experts, k, min_weight_sum, ids, weights, probs);
   } else if (per <= 2) {
     hipLaunchKernelGGL(router_topk_kernel<2>, dim3(blocks), dim3(256), 0, st, logits, tokens,
-                       experts, k, min_weight_sum, ids, weights);
+                       experts, k, min_weight_sum, ids, weights, probs);
   } else if (per <= 4) {
     hipLaunchKernelGGL(router_topk_kernel<4>, dim3(blocks), dim3(256), 0, st, logits, tokens,
-                       experts, k, min_weight_sum, ids, weights);
+                       experts, k, min_weight_sum, ids, weights, probs);
   } else if (per <= 8) {
     hipLaunchKernelGGL(router_topk_kernel<8>, dim3(blocks), dim3(256), 0, st, logits, tokens,
-                       experts, k, min_weight_sum, ids, weights);
+                       experts, k, min_weight_sum, ids, weights, probs);
   } else {
     hipLaunchKernelGGL(router_topk_kernel<kRouterMaxPerLane>, dim3(blocks), dim3(256), 0, st,
-                       logits, tokens, experts, k, min_weight_sum, ids, weights);
+                       logits, tokens, experts, k, min_weight_sum, ids, weights, probs);
   }
 }
 
+// probs (nullable): the picks' softmax probabilities before renormalization.
 int router_topk_launch(const float* logits, int64_t tokens, int experts, int k,
-                       float min_weight_sum, int32_t* ids, float* weights, hipStream_t st) {
-  launch_router_topk(logits, tokens, experts, k, min_weight_sum, ids, weights, st);
+                       float min_weight_sum, int32_t* ids, float* weights, hipStream_t st,
+                       float* probs) {
+  launch_router_topk(logits, tokens, experts, k, min_weight_sum, ids, weights, st, probs);
   return launch_check("router_topk");
 }
 

@@ -9,6 +9,9 @@ replace:
 * ``select_router_topk``   <- ``select_router_topk`` (gguf_loader.hpp:371-373)
 * ``run_moe_ffn_layer``    <- ``run_qwen36_moe_ffn_layer``'s expert part
   (gguf_loader.hpp:519-524, gguf_loader.cpp:5711-5780)
+* ``ffn_layer_trace``      <- ``run_qwen36_moe_ffn_layer`` with its
+  ``Qwen36MoeFfnLayerResult`` / ``RouterTopKSelection`` records
+  (gguf_loader.hpp:138-161)
 * ``grouped_moe_prefill``  <- ``GroupedS8U4PrefillRuntime::RunLayer`` /
   ``MOE3GemmFusedCompressed``
 * ``build_grouped_schedule`` <- ``BuildGroupedSchedule``
@@ -23,6 +26,7 @@ are flagged in the workspace error word on the device (the reference throws
 from __future__ import annotations
 
 import ctypes as C
+from dataclasses import dataclass
 from typing import Optional, Sequence
 
 import torch
@@ -324,6 +328,88 @@ def run_moe_ffn_layer(layer: MoeLayerWeights, x: torch.Tensor, ids: torch.Tensor
     call("aima_moe_ffn_decode", C.byref(lc), x.data_ptr(), _ptr(residual), ids.data_ptr(),
          weights.data_ptr(), k, out.data_ptr(), buf.data_ptr(), buf.numel(), _stream())
     return out
+
+
+@dataclass
+class RouterTopKSelection:
+    """``RouterTopKSelection`` (gguf_loader.hpp:138-142), as device tensors."""
+    expert_ids: torch.Tensor          # int32 [k]
+    weights: torch.Tensor             # float32 [k] softmax probabilities of the picks
+    normalized_weights: torch.Tensor  # float32 [k]
+
+
+@dataclass
+class Qwen36MoeFfnLayerResult:
+    """``Qwen36MoeFfnLayerResult`` (gguf_loader.hpp:144-161), as device
+    tensors: every intermediate of one decode FFN layer (ffn_layer_trace)."""
+    ffn_norm: torch.Tensor                # float16 [H] (the decode kernels' input)
+    router_logits: torch.Tensor           # float32 [E]
+    router: RouterTopKSelection
+    selected_gate_up: torch.Tensor        # float32 [k * 2I] gate rows, then up rows, per pick
+    selected_swiglu: torch.Tensor         # float16 [k * I]
+    selected_down: torch.Tensor           # float32 [k * H]
+    weighted_selected_down: torch.Tensor  # float32 [k * H]
+    moe_out: torch.Tensor                 # float32 [H]
+    shared_gate: torch.Tensor             # float32 [1]
+    shared_gate_sigmoid: torch.Tensor     # float32 [1]
+    shared_gate_up: torch.Tensor          # float32 [2I]
+    shared_swiglu: torch.Tensor           # float16 [I]
+    shared_down: torch.Tensor             # float32 [H]
+    shared_gated: torch.Tensor            # float32 [H]
+    ffn_out: torch.Tensor                 # float32 [H]
+    residual: torch.Tensor                # float16 [H] (the layer's output)
+
+
+def ffn_layer_trace(layer: MoeLayerWeights, router: U4Weight, residual: torch.Tensor,
+                    epsilon: float = 1e-6, expert_used_count: int = 8,
+                    min_weight_sum: float = MIN_WEIGHT_SUM,
+                    ws: Optional[Workspace] = None) -> Qwen36MoeFfnLayerResult:
+    """One decode FFN layer from its residual input with every intermediate,
+    the counterpart of run_qwen36_moe_ffn_layer (gguf_loader.cpp:5654-5782):
+    RMSNorm, router FC and selection, the two decode kernels (their own
+    gate/up rows, activations, per-pick down rows and shared gate captured)
+    and the rank-order sums.  A debugging path; the fast paths do not keep
+    these."""
+    _require_cuda(residual, router.qweight)
+    H, I, E = layer.hidden, layer.inter, layer.experts
+    if residual.dtype != torch.float16 or residual.numel() != H or not residual.is_contiguous():
+        raise ValueError("residual must be a contiguous float16 [hidden] vector")
+    if layer.norm_weight is None:
+        raise ValueError("the layer needs its norm weight")
+    if router.experts * router.rows != E or router.k != H or router.group != layer.group:
+        raise ValueError("router must be U4 [experts][hidden] with the layer's group")
+    k = int(expert_used_count)
+    dev = residual.device
+
+    def f32(n):
+        return torch.empty(n, dtype=torch.float32, device=dev)
+
+    def f16(n):
+        return torch.empty(n, dtype=torch.float16, device=dev)
+
+    r = Qwen36MoeFfnLayerResult(
+        ffn_norm=f16(H), router_logits=f32(E),
+        router=RouterTopKSelection(torch.empty(k, dtype=torch.int32, device=dev), f32(k), f32(k)),
+        selected_gate_up=f32(k * 2 * I), selected_swiglu=f16(k * I), selected_down=f32(k * H),
+        weighted_selected_down=f32(k * H), moe_out=f32(H), shared_gate=f32(1),
+        shared_gate_sigmoid=f32(1), shared_gate_up=f32(2 * I), shared_swiglu=f16(I),
+        shared_down=f32(H), shared_gated=f32(H), ffn_out=f32(H), residual=f16(H))
+    t = _lib.FfnTraceC(
+        r.ffn_norm.data_ptr(), r.router_logits.data_ptr(), r.router.expert_ids.data_ptr(),
+        r.router.weights.data_ptr(), r.router.normalized_weights.data_ptr(),
+        r.selected_gate_up.data_ptr(), r.selected_swiglu.data_ptr(), r.selected_down.data_ptr(),
+        r.weighted_selected_down.data_ptr(), r.moe_out.data_ptr(), r.shared_gate.data_ptr(),
+        r.shared_gate_sigmoid.data_ptr(), r.shared_gate_up.data_ptr(), r.shared_swiglu.data_ptr(),
+        r.shared_down.data_ptr(), r.shared_gated.data_ptr(), r.ffn_out.data_ptr(),
+        r.residual.data_ptr())
+    lc = layer.c()
+    rt = _lib.U4TensorC(router.qweight.data_ptr(), router.scale.data_ptr(), router.zp.data_ptr())
+    ws = _ws(ws, dev)
+    buf = ws.get(size_query("aima_moe_ffn_layer_trace_workspace_size", C.byref(lc), k))
+    call("aima_moe_ffn_layer_trace", C.byref(lc), C.byref(rt), residual.data_ptr(),
+         float(epsilon), k, float(min_weight_sum), C.byref(t), buf.data_ptr(), buf.numel(),
+         _stream())
+    return r
 
 
 def moe_decode_gate_up(layer: MoeLayerWeights, x: torch.Tensor, ids: torch.Tensor,

@@ -247,6 +247,50 @@ int aima_moe_ffn_decode(const aima_moe_layer* layer, const uint16_t* x,
                         const float* weights, int32_t k, uint16_t* out,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Every intermediate of one decode FFN layer, as device buffers the caller
+ * owns: the counterpart of Qwen36MoeFfnLayerResult and RouterTopKSelection
+ * (engine/include/intel_qwen36/gguf_loader.hpp:138-161), filled by
+ * aima_moe_ffn_layer_trace.  Sizes: H = hidden, I = inter, E = experts. */
+typedef struct aima_ffn_trace {
+  uint16_t* ffn_norm;             /* f16[H]  rmsnorm(residual): the layer's input */
+  float* router_logits;           /* f32[E] */
+  int32_t* expert_ids;            /* [k]     RouterTopKSelection.expert_ids */
+  float* router_weights;          /* [k]     .weights (softmax probabilities) */
+  float* normalized_weights;      /* [k]     .normalized_weights */
+  float* selected_gate_up;        /* [k][2I] gate rows, then up rows, per pick */
+  uint16_t* selected_swiglu;      /* f16[k][I] (the down projections' input) */
+  float* selected_down;           /* [k][H]  unweighted */
+  float* weighted_selected_down;  /* [k][H] */
+  float* moe_out;                 /* [H]     rank-order sum of the weighted rows */
+  float* shared_gate;             /* [1]     shared_gate_vec . ffn_norm */
+  float* shared_gate_sigmoid;     /* [1] */
+  float* shared_gate_up;          /* [2I] */
+  uint16_t* shared_swiglu;        /* f16[I] */
+  float* shared_down;             /* [H] */
+  float* shared_gated;            /* [H] */
+  float* ffn_out;                 /* [H]     moe_out + shared_gated */
+  uint16_t* residual;             /* f16[H]  the layer's output, as aima_moe_ffn_decode */
+} aima_ffn_trace;
+
+/* Workspace bytes for aima_moe_ffn_layer_trace. */
+int aima_moe_ffn_layer_trace_workspace_size(const aima_moe_layer* layer, int32_t k,
+                                            size_t* bytes);
+
+/* One decode FFN layer with every intermediate kept (a debugging path, not
+ * the fast one): ffn_norm = rmsnorm(residual, layer->norm_weight, eps); the
+ * router (U4 [experts][hidden], the layer's group) and its selection as
+ * aima_router_fc_topk; then aima_moe_ffn_decode's two kernels with their
+ * gate/up rows, activations, per-pick down rows and shared gate captured,
+ * and the weighted sums formed in rank order.  Mirrors
+ * run_qwen36_moe_ffn_layer (engine/src/gguf_loader.cpp:5654-5782).  `residual`
+ * is the kernels' own output (their summation order differs from the rank
+ * order of moe_out/ffn_out by f32 rounding only).  Every buffer of *trace is
+ * required; experts <= 1024, k <= 16. */
+int aima_moe_ffn_layer_trace(const aima_moe_layer* layer, const aima_u4_tensor* router,
+                             const uint16_t* residual, float eps, int32_t k,
+                             float min_weight_sum, const aima_ffn_trace* trace,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
 /* The two launches of aima_moe_ffn_decode, separately.
  * Gate/up: act[r][j] = f16(silu(g) * u) for the k routed experts (slot r =
  * ids[r]) and the shared expert (slot k), act f16 [k+1][inter], plus the
