@@ -32,6 +32,7 @@ from .ops import (  # noqa: F401
     prefill_workspace_views,
     q4k_unpack,
     router_fc_topk,
+    router_gemm_topk,
     run_moe_ffn_layer,
     select_router_topk,
     topk_f32,

@@ -84,6 +84,9 @@ SIGNATURES = {
                                        _i32, C.POINTER(_vp), C.POINTER(_i32), _vp]),
     "aima_router_fc_topk": (C.c_int, [_vp, C.POINTER(U4TensorC), _i32, _i64, _i32, _i32, _f32,
                                       _vp, _vp, _vp, _vp]),
+    "aima_router_gemm_workspace_size": (C.c_int, [_i64, _i64, _i32, _szp]),
+    "aima_router_gemm_topk": (C.c_int, [_vp, _i32, _i64, _i64, _vp, _i32, _i32, _f32, _vp, _vp,
+                                        _vp, _vp, C.c_size_t, _vp]),
     "aima_u4_group_major_to_rows": (C.c_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "aima_u4_rows_to_group_major": (C.c_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "aima_q4k_unpack": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),

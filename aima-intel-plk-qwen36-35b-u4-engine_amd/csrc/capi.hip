@@ -31,7 +31,7 @@ int launch_check(const char* what) {
 
 extern "C" const char* aima_last_error(void) { return aima::g_last_error.c_str(); }
 
-extern "C" int aima_version(void) { return 101; }
+extern "C" int aima_version(void) { return 102; }
 
 extern "C" int aima_workspace_error(void* workspace, uint32_t* error_bits, void* stream) {
   AIMA_REQUIRE(workspace && error_bits, "workspace_error: null pointer");

@@ -184,6 +184,38 @@ def router_fc_topk(h: torch.Tensor, router: U4Weight, expert_used_count: int = 8
     return ids, w, logits
 
 
+def router_gemm_topk(hidden_states: torch.Tensor, router_weight: torch.Tensor,
+                     expert_used_count: int = 8, min_weight_sum: float = MIN_WEIGHT_SUM,
+                     ws: Optional[Workspace] = None):
+    """Routing of a batch of tokens on the device (the grouped prefill's
+    native router, grouped_s8_u4_prefill_runtime.cpp:1085-1101): logits =
+    hidden_states [T, H] (float32 or float16) . router_weight [E, H]^T
+    (float32), then select_router_topk per token.  Returns (ids int32
+    [T, k], weights float32 [T, k], logits float32 [T, E])."""
+    _require_cuda(hidden_states, router_weight)
+    if hidden_states.dim() != 2 or hidden_states.dtype not in (torch.float32, torch.float16):
+        raise ValueError("hidden_states must be float32 or float16 [tokens, hidden]")
+    if router_weight.dtype != torch.float32 or router_weight.dim() != 2 or \
+            router_weight.shape[1] != hidden_states.shape[1]:
+        raise ValueError("router_weight must be float32 [experts, hidden]")
+    x = hidden_states.contiguous()
+    wt = router_weight.contiguous()
+    T, H = x.shape
+    E = wt.shape[0]
+    k = int(expert_used_count)
+    f32 = 1 if x.dtype == torch.float32 else 0
+    dev = x.device
+    logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+    ids = torch.empty((T, k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    need = size_query("aima_router_gemm_workspace_size", T, H, f32)
+    buf = _ws(ws, dev).get(need) if need else None
+    call("aima_router_gemm_topk", x.data_ptr(), f32, T, H, wt.data_ptr(), E, k,
+         float(min_weight_sum), logits.data_ptr(), ids.data_ptr(), w.data_ptr(),
+         _ptr(buf), 0 if buf is None else buf.numel(), _stream())
+    return ids, w, logits
+
+
 def u4_group_major_to_rows(scale_gm: torch.Tensor, zp_gm: torch.Tensor, n: int, groups: int):
     """Group-major scale f16 [groups][n] and zero points (packed over the
     group-major flat index) -> the boundary row-major order."""

@@ -16,7 +16,10 @@ residual.  Differences: the weights are already U4 tensors on the device (no
 prep directory), inputs are device tensors, the schedule is always built on
 the device (the reference's ``device_schedule``), and timing uses HIP events
 on the current stream.  Intermediates come from the last timed repeat's own
-workspace, not from a second run.
+workspace, not from a second run.  ``native_router`` routes the tokens on the
+device from the hidden states with the layer's f32 router (one GEMM and the
+top-k selection, inside each timed repeat) as the reference runtime's native
+router does.
 """
 
 from __future__ import annotations
@@ -30,8 +33,9 @@ import torch
 from . import ops
 from .layout import MoeLayerWeights
 
-# stage_us[i]: schedule, gate/up GEMM + SwiGLU, down GEMM, combine
-STAGES = ("schedule", "gate_up", "down", "combine")
+# stage_us[i]: native router (0 without it), schedule, gate/up GEMM + SwiGLU,
+# down GEMM, combine
+STAGES = ("router", "schedule", "gate_up", "down", "combine")
 
 
 @dataclass
@@ -46,6 +50,10 @@ class GroupedU4PrefillInput:
     capture_intermediates: bool = False
     include_shared: bool = False         # extension: f16 routed + shared (+ residual)
     residual: Optional[torch.Tensor] = None
+    # route every token on the device from hidden_states with the layer's
+    # resident f32 router (LoadLayer(..., router_weight=...)); topk and
+    # router_weights are then ignored (grouped_s8_u4_prefill_runtime.hpp:80-83)
+    native_router: bool = False
 
 
 @dataclass
@@ -78,17 +86,28 @@ class GroupedU4PrefillRuntime:
     def __init__(self, device=None):
         self.device = torch.device("cuda") if device is None else torch.device(device)
         self._layers: Dict[int, MoeLayerWeights] = {}
+        self._routers: Dict[int, torch.Tensor] = {}
         self._next = 1
         self._ws = ops.Workspace(self.device)
         self._stats = {"layer_load_count": 0, "layer_count": 0, "run_count": 0,
-                       "resident_weight_bytes": 0, "device_schedule_run_count": 0}
+                       "resident_weight_bytes": 0, "device_schedule_run_count": 0,
+                       "native_router_run_count": 0}
 
-    def LoadLayer(self, weights: MoeLayerWeights) -> int:
+    def LoadLayer(self, weights: MoeLayerWeights,
+                  router_weight: Optional[torch.Tensor] = None) -> int:
+        """router_weight: the layer's f32 router [experts, hidden] for
+        native_router runs (the reference's layer router_weights path)."""
         if weights.gate_up.qweight.device.type != "cuda":
             weights = _to_device(weights, self.device)
         handle = self._next
         self._next += 1
         self._layers[handle] = weights
+        if router_weight is not None:
+            if router_weight.dtype != torch.float32 or \
+                    tuple(router_weight.shape) != (weights.experts, weights.hidden):
+                raise ValueError("router_weight must be float32 [experts, hidden]")
+            self._routers[handle] = router_weight.to(self.device).contiguous()
+            self._stats["resident_weight_bytes"] += router_weight.numel() * 4
         self._stats["layer_load_count"] += 1
         self._stats["layer_count"] = len(self._layers)
         self._stats["resident_weight_bytes"] += (weights.gate_up.nbytes + weights.down.nbytes +
@@ -109,7 +128,14 @@ class GroupedU4PrefillRuntime:
         if x.dim() != 2 or x.shape[1] != layer.hidden:
             raise ValueError("grouped prefill hidden-state count mismatch")
         T, k = x.shape[0], int(inp.expert_used_count)
-        if inp.router_weights.numel() != T * k:
+        router = None
+        if inp.native_router:
+            if handle not in self._routers:
+                raise ValueError("native_router needs a layer loaded with its router weight")
+            if inp.include_shared:
+                raise ValueError("native_router runs return the routed sum")
+            router = self._routers[handle]
+        elif inp.router_weights.numel() != T * k:
             raise ValueError("grouped prefill router weight count mismatch")
         stride = inp.topk_stride or None
         if inp.include_shared:
@@ -118,6 +144,7 @@ class GroupedU4PrefillRuntime:
             if x.dtype != torch.float16:
                 raise ValueError("include_shared takes float16 hidden states")
 
+        # events: router start, then the prefill call's own five
         stage_events = [torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)]
 
         def execute(events=None):
@@ -125,9 +152,16 @@ class GroupedU4PrefillRuntime:
                 return ops.grouped_moe_prefill(layer, x, inp.topk,
                                                inp.router_weights.reshape(T, k),
                                                residual=inp.residual, ws=self._ws)
-            return ops.grouped_moe_prefill_routed(layer, x, inp.topk, inp.router_weights,
-                                                  topk_stride=stride, expert_used_count=k,
-                                                  ws=self._ws, stage_events=events)
+            topk, rw, st = inp.topk, inp.router_weights, stride
+            if events is not None:
+                events[0].record(torch.cuda.current_stream())
+            if router is not None:
+                topk, rw, _ = ops.router_gemm_topk(x, router, k, ws=self._ws)
+                rw, st = rw.reshape(-1), None
+            return ops.grouped_moe_prefill_routed(layer, x, topk, rw, topk_stride=st,
+                                                  expert_used_count=k, ws=self._ws,
+                                                  stage_events=None if events is None
+                                                  else events[1:])
 
         for _ in range(inp.warmup):
             execute()
@@ -152,7 +186,7 @@ class GroupedU4PrefillRuntime:
                                         mean_us=statistics.fmean(samples))
         if stages:
             timing.stage_us = [statistics.median(s[i] for s in stages) for i in range(len(STAGES))]
-        run = GroupedU4PrefillRun(output=out, timing=timing)
+        run = GroupedU4PrefillRun(output=out, timing=timing, native_router=router is not None)
         if inp.capture_intermediates:
             # the last repeat's schedule and intermediates, still in the workspace
             v = ops.prefill_workspace_views(layer, T, k, self._ws, with_shared=inp.include_shared)
@@ -168,6 +202,8 @@ class GroupedU4PrefillRuntime:
             run.max_group_size = int(counts.max().item())
         self._stats["run_count"] += 1
         self._stats["device_schedule_run_count"] += 1
+        if router is not None:
+            self._stats["native_router_run_count"] += 1
         return run
 
     def stats(self) -> dict:

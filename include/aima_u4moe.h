@@ -174,6 +174,24 @@ int aima_router_fc_topk(const uint16_t* h, const aima_u4_tensor* router,
                         int32_t k, float min_weight_sum, float* logits,
                         int32_t* ids, float* weights, void* stream);
 
+/* Workspace bytes for aima_router_gemm_topk (0 for an f32 input). */
+int aima_router_gemm_workspace_size(int64_t tokens, int64_t hidden,
+                                    int32_t input_f32, size_t* bytes);
+
+/* Router for a batch of tokens (the grouped prefill's native router,
+ * grouped_s8_u4_prefill_runtime.cpp:1085-1101; its weights are f32,
+ * kRouterWeightBytes = experts x hidden x 4 at :35): logits[T][E] =
+ * hidden_states[T][H] . router_weight[E][H]^T in f32 (rocBLAS sgemm on
+ * `stream`), then the selection of aima_router_topk per token: ids[T][k],
+ * weights[T][k] (normalized).  hidden_states is f32 (input_f32 = 1) or f16
+ * (0: widened to f32 in the workspace first).  experts <= 1024, k <= 16. */
+int aima_router_gemm_topk(const void* hidden_states, int32_t input_f32,
+                          int64_t tokens, int64_t hidden,
+                          const float* router_weight, int32_t experts, int32_t k,
+                          float min_weight_sum, float* logits, int32_t* ids,
+                          float* weights, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* Scale / zero-point order conversions for an [n][groups] U4 matrix: the
  * boundary order is row-major (scale f16[n][groups], zero points over the
  * flat n*groups index, low nibble first), which is also the order of an

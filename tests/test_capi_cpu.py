@@ -40,7 +40,7 @@ def test_library_shares_torch_hip_runtime(pkg):
 
 def test_version_and_error_paths(pkg):
     L = pkg._lib.lib()
-    assert L.aima_version() == 101
+    assert L.aima_version() == 102
     rc = L.aima_u4_matvec(None, None, None, None, 4, 2048, 128, None, 0, None)
     assert rc == pkg._lib.AIMA_E_INVALID
     assert b"null pointer" in L.aima_last_error()

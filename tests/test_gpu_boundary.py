@@ -133,7 +133,9 @@ def test_run_layer_intermediates_and_stages(pkg, dev, layer_c2):
     run = rt.RunLayer(h, pkg.GroupedU4PrefillInput(x, ids, w.reshape(-1), warmup=1, repeat=3,
                                                    capture_intermediates=True))
     assert run.output.dtype == torch.float32 and run.output.shape == (T, 2048)
-    assert len(run.timing.stage_us) == 4 and all(s > 0 for s in run.timing.stage_us)
+    # router (no native router here: ~0), schedule, gate/up, down, combine
+    assert len(run.timing.stage_us) == 5 and all(s > 0 for s in run.timing.stage_us[1:])
+    assert not run.native_router
     assert sum(run.timing.stage_us) <= max(run.timing.samples_us) * 1.1 + 5
     sched = oracle.build_grouped_schedule(ids.cpu().numpy(), 256, w.cpu().numpy())
     assert np.array_equal(run.inverse_map.cpu().numpy(), sched["inverse_map"])
