@@ -31,6 +31,7 @@ from .ops import (  # noqa: F401
     moe_stack_prefill,
     prefill_workspace_views,
     q4k_unpack,
+    q4s_matvec,
     router_fc_topk,
     router_gemm_topk,
     run_moe_ffn_layer,

@@ -90,6 +90,7 @@ SIGNATURES = {
     "aima_u4_group_major_to_rows": (C.c_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "aima_u4_rows_to_group_major": (C.c_int, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
     "aima_q4k_unpack": (C.c_int, [_vp, _i64, _i64, _vp, _vp, _vp, _vp]),
+    "aima_q4s_matvec": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp]),
     "aima_topk_workspace_size": (C.c_int, [_i64, _i32, _szp]),
     "aima_topk_f32": (C.c_int, [_vp, _i64, _i32, _vp, _vp, _vp, C.c_size_t, _vp]),
     "aima_u4_lm_head_topk": (C.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp,

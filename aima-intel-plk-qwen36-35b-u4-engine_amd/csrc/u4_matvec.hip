@@ -203,6 +203,109 @@ __device__ __forceinline__ void matvec_block(
   }
 }
 
+// Scale-and-min U4 rows (the Q4_K-derived form, groups of 32: one per
+// 16-byte chunk): w = q * s - m with f16 s and f32 m per group, row-major
+// [n][k/32] each.  y[n] = sum_g (s_g * sum q x - m_g * sum x) over the row's
+// groups, the min applied to each group's activation sum as the reference's
+// micro runtime applies it after its GEMM (openvino_moe_micro_runtime.cpp:
+// 735-745, input_sums and mins).  Same block geometry and load order as
+// matvec_block.
+template <int KCH, int RG>
+__device__ __forceinline__ void q4s_matvec_block(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ qw,
+    const uint16_t* __restrict__ scale, const float* __restrict__ mins, int64_t n,
+    void* __restrict__ y, int out_f32, int64_t blk) {
+  using G = RowGeom<KCH>;
+  constexpr int BR = 4 * RG * G::RPI;
+  constexpr int kGroups = G::K / 32;  // groups (chunks) per row
+  constexpr int kSW = (BR * kGroups / 2 + 255) / 256;
+  constexpr int kMW = (BR * kGroups + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t s_lds[BR * kGroups];
+  __shared__ __attribute__((aligned(16))) float m_lds[BR * kGroups];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int seg = lane / G::SEG;
+  const int cl = lane % G::SEG;
+  const uint32_t magic = u4_magic();
+  const int64_t brow0 = blk * BR;
+  const int64_t row0 = brow0 + (int64_t)wave * (RG * G::RPI);
+  const int64_t rows_here = n - brow0 < BR ? n - brow0 : BR;
+  const int nsc = (int)rows_here * kGroups;
+  const uint16_t* sblk = scale + brow0 * kGroups;
+  const float* mblk = mins + brow0 * kGroups;
+  const bool s_words = (reinterpret_cast<uintptr_t>(sblk) & 3u) == 0;
+  const int s_full = s_words ? nsc / 2 : 0;
+  uint32_t sw[kSW];
+  float mw[kMW];
+#pragma unroll
+  for (int j = 0; j < kSW; ++j) {
+    const int i = tid + 256 * j;
+    sw[j] = i < s_full ? reinterpret_cast<const uint32_t*>(sblk)[i] : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < kMW; ++j) {
+    const int i = tid + 256 * j;
+    mw[j] = i < nsc ? mblk[i] : 0.f;
+  }
+  u32x4 xr[G::NC][4];
+  load_x_raw<KCH>(x, cl, xr);
+  u32x4 w[RG][G::NC];
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int64_t row = row0 + r * G::RPI + seg;
+    const int64_t rowc = row < n ? row : n - 1;
+#pragma unroll
+    for (int i = 0; i < G::NC; ++i) {
+      const int c = cl + i * G::SEG;
+      w[r][i] = load16_nt(qw + rowc * (G::K / 2) + (int64_t)c * 16);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < kSW; ++j) {
+    const int i = tid + 256 * j;
+    if (i < s_full) reinterpret_cast<uint32_t*>(s_lds)[i] = sw[j];
+  }
+#pragma unroll
+  for (int j = 0; j < kMW; ++j) {
+    const int i = tid + 256 * j;
+    if (i < nsc) m_lds[i] = mw[j];
+  }
+  for (int t = 2 * s_full + tid; t < nsc; t += 256) s_lds[t] = sblk[t];
+  XChunk xc[G::NC];
+  build_x_chunks<KCH>(xr, xc);
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < RG; ++r) {
+    const int rl = wave * (RG * G::RPI) + r * G::RPI + seg;
+    const int64_t row = brow0 + rl;
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < G::NC; ++i) {
+      const int gi = rl * kGroups + cl + i * G::SEG;  // chunk c = group c
+      const float sv = row < n ? h2f(s_lds[gi]) : 0.f;
+      const float mv = row < n ? m_lds[gi] : 0.f;
+      acc += u4_chunk_dot(w[r][i], xc[i], 0u, sv, magic) - mv * xc[i].xsum;
+    }
+    acc = segment_sum<G::SEG>(acc);
+    if (cl == 0 && row < n) {
+      if (out_f32) {
+        reinterpret_cast<float*>(y)[row] = acc;
+      } else {
+        reinterpret_cast<uint16_t*>(y)[row] = f2h(acc);
+      }
+    }
+  }
+}
+
+template <int KCH, int RG>
+__global__ __launch_bounds__(256) void q4s_matvec_kernel(
+    const uint16_t* __restrict__ x, const uint8_t* __restrict__ qw,
+    const uint16_t* __restrict__ scale, const float* __restrict__ mins, int64_t n,
+    void* __restrict__ y, int out_f32) {
+  q4s_matvec_block<KCH, RG>(x, qw, scale, mins, n, y, out_f32, blockIdx.x);
+}
+
 template <int KCH, int RG>
 __global__ __launch_bounds__(256) void u4_matvec_kernel(
     const uint16_t* __restrict__ x, const uint8_t* __restrict__ qw,
@@ -254,6 +357,22 @@ static void launch_matvec(const uint16_t* x, const uint8_t* qw, const uint16_t* 
     const int64_t rows4 = 4 * 4 * RowGeom<KCH>::RPI;
     hipLaunchKernelGGL((u4_matvec_kernel<KCH, 4>), dim3((unsigned)((n + rows4 - 1) / rows4)),
                        dim3(256), 0, st, x, qw, scale, zp, n, glog2, y, out_f32);
+  }
+}
+
+template <int KCH>
+static void launch_q4s_matvec(const uint16_t* x, const uint8_t* qw, const uint16_t* scale,
+                              const float* mins, int64_t n, void* y, int out_f32,
+                              hipStream_t st) {
+  // the row-group rule of launch_matvec
+  const int64_t rows8 = 4 * 8 * RowGeom<KCH>::RPI;
+  if ((n + rows8 - 1) / rows8 >= 512) {
+    hipLaunchKernelGGL((q4s_matvec_kernel<KCH, 8>), dim3((unsigned)((n + rows8 - 1) / rows8)),
+                       dim3(256), 0, st, x, qw, scale, mins, n, y, out_f32);
+  } else {
+    const int64_t rows4 = 4 * 4 * RowGeom<KCH>::RPI;
+    hipLaunchKernelGGL((q4s_matvec_kernel<KCH, 4>), dim3((unsigned)((n + rows4 - 1) / rows4)),
+                       dim3(256), 0, st, x, qw, scale, mins, n, y, out_f32);
   }
 }
 
@@ -504,6 +623,30 @@ extern "C" int aima_u4_matvec(const uint16_t* x, const uint8_t* qweight,
                "u4_matvec: qweight and x must be 16-byte aligned");
   return u4_matvec_dispatch(x, qweight, scale, zp, n, k, glog2, y, out_dtype,
                             (hipStream_t)stream);
+}
+
+extern "C" int aima_q4s_matvec(const uint16_t* x, const uint8_t* codes, const uint16_t* scale,
+                               const float* mins, int64_t n, int64_t k, void* y,
+                               int32_t out_dtype, void* stream) {
+  AIMA_REQUIRE(x && codes && scale && mins && y, "q4s_matvec: null pointer");
+  AIMA_REQUIRE(n > 0, "q4s_matvec: n must be positive");
+  AIMA_REQUIRE(out_dtype == AIMA_OUT_F16 || out_dtype == AIMA_OUT_F32,
+               "q4s_matvec: out_dtype must be AIMA_OUT_F16 or AIMA_OUT_F32");
+  AIMA_REQUIRE(aligned(codes, 16) && aligned(x, 16) && aligned(mins, 4),
+               "q4s_matvec: codes and x must be 16-byte aligned, mins 4-byte aligned");
+  const hipStream_t st = (hipStream_t)stream;
+  switch (k) {
+    case 128: launch_q4s_matvec<4>(x, codes, scale, mins, n, y, out_dtype, st); break;
+    case 256: launch_q4s_matvec<8>(x, codes, scale, mins, n, y, out_dtype, st); break;
+    case 512: launch_q4s_matvec<16>(x, codes, scale, mins, n, y, out_dtype, st); break;
+    case 1024: launch_q4s_matvec<32>(x, codes, scale, mins, n, y, out_dtype, st); break;
+    case 2048: launch_q4s_matvec<64>(x, codes, scale, mins, n, y, out_dtype, st); break;
+    case 4096: launch_q4s_matvec<128>(x, codes, scale, mins, n, y, out_dtype, st); break;
+    case 8192: launch_q4s_matvec<256>(x, codes, scale, mins, n, y, out_dtype, st); break;
+    default:
+      return fail(AIMA_E_UNSUPPORTED, "q4s_matvec: K must be a power of two in [128, 8192]");
+  }
+  return launch_check("q4s_matvec");
 }
 
 extern "C" int aima_u4_matvec_multi(const uint16_t* x, int32_t count,

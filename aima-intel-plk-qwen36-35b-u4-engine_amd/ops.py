@@ -262,6 +262,25 @@ def q4k_unpack(blocks: torch.Tensor, rows: int, cols: int):
     return q, sc, mn
 
 
+def q4s_matvec(x: torch.Tensor, codes: torch.Tensor, scale: torch.Tensor, mins: torch.Tensor,
+               out_dtype=torch.float32) -> torch.Tensor:
+    """Matvec over q4k_unpack's output (codes uint8 [n, k/2], scale float16
+    [n, k/32], mins float32 [n, k/32]): y = sum (scale * q - min) * x."""
+    _require_cuda(x, codes, scale, mins)
+    n, k = codes.shape[0], codes.shape[1] * 2
+    if x.dtype != torch.float16 or x.numel() != k or not x.is_contiguous():
+        raise ValueError("x must be a contiguous float16 vector of length k")
+    if codes.dtype != torch.uint8 or scale.dtype != torch.float16 or mins.dtype != torch.float32:
+        raise TypeError("codes uint8, scale float16, mins float32")
+    if scale.shape != (n, k // 32) or mins.shape != (n, k // 32):
+        raise ValueError("scale and mins must be [n, k/32]")
+    y = torch.empty(n, dtype=out_dtype, device=x.device)
+    call("aima_q4s_matvec", x.data_ptr(), codes.contiguous().data_ptr(),
+         scale.contiguous().data_ptr(), mins.contiguous().data_ptr(), n, k, y.data_ptr(),
+         _lib.AIMA_OUT_F32 if out_dtype == torch.float32 else _lib.AIMA_OUT_F16, _stream())
+    return y
+
+
 def topk_f32(values: torch.Tensor, k: int, ws: Optional[Workspace] = None):
     """Top-k of a float32 vector on the device: (ids int32 [k], values float32
     [k]), value descending, lower index first among equal values."""

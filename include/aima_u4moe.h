@@ -213,11 +213,23 @@ int aima_u4_rows_to_group_major(const uint16_t* scale, const uint8_t* zp,
  * (f32[rows][cols/32]); the value is scale * q - min.  The package the
  * reference's prepack builds from Q4_K
  * (tools/intel-qwen36-openvino-moe-micro-prepack.py:76-124), row-major.
- * cols % 256 == 0.  (The boundary matvec takes integer zero points, not
- * mins: Q4_K weights reach it only through a requantization, not done here.) */
+ * cols % 256 == 0.  aima_q4s_matvec consumes this form directly. */
 int aima_q4k_unpack(const uint8_t* blocks, int64_t rows, int64_t cols,
                     uint8_t* qweight, uint16_t* scale, float* mins,
                     void* stream);
+
+/* Matvec over the scale-and-min form that aima_q4k_unpack produces (the
+ * reference's prepacked Q4_K, tools/intel-qwen36-openvino-moe-micro-prepack.py
+ * :91-176): y[n] = sum_k (f32(scale[n][k/32]) * q[n][k] - mins[n][k/32]) * x[k],
+ * computed per 32-wide group as scale * sum(q x) - min * sum(x) -- the
+ * reference's micro runtime applies the mins to the per-group input sums
+ * after its GEMM (engine/tools/openvino_moe_micro_runtime.cpp:735-745).
+ * codes u8 [n][k/2] (aima_u4_matvec's packing), scale f16 and mins f32
+ * [n][k/32] row-major; f16 or f32 output.  K = 32 * 2^j with
+ * 128 <= K <= 8192; codes and x 16-byte aligned. */
+int aima_q4s_matvec(const uint16_t* x, const uint8_t* codes,
+                    const uint16_t* scale, const float* mins, int64_t n,
+                    int64_t k, void* y, int32_t out_dtype, void* stream);
 
 /* Workspace bytes for aima_topk_f32 / aima_u4_lm_head_topk over n values. */
 int aima_topk_workspace_size(int64_t n, int32_t k, size_t* bytes);

@@ -352,6 +352,23 @@ def q4k_unpack(raw, rows: int, cols: int, f32_scale: bool = False):
     return packed, scale, mn.reshape(rows, bpr * 8)
 
 
+def q4s_dequant(codes, scale_bits, mins, n: int, k: int) -> np.ndarray:
+    """The scale-and-min form (q4k_unpack's output) -> f32 weights
+    value = f32(scale) * q - min, per 32-wide group
+    (tools/intel-qwen36-openvino-moe-micro-prepack.py:91-124: the prepacked
+    scale = d * sc rounded to f16, min = dmin * m in f32)."""
+    q = u4_nibbles(codes, n * k).reshape(n, k).astype(np.float32)
+    s = half_to_float(np.asarray(scale_bits, np.uint16).reshape(-1)).reshape(n, k // 32)
+    m = np.asarray(mins, np.float32).reshape(n, k // 32)
+    return (q * np.repeat(s, 32, axis=1)).astype(np.float32) - np.repeat(m, 32, axis=1)
+
+
+def q4s_matvec(codes, scale_bits, mins, n: int, k: int, x) -> np.ndarray:
+    """y = q4s_dequant(...) . x, the products and sum in float64."""
+    w = q4s_dequant(codes, scale_bits, mins, n, k).astype(np.float64)
+    return (w @ _f32(x).reshape(-1).astype(np.float64)).astype(np.float32)
+
+
 def normalize_weights(w, min_weight_sum: float) -> np.ndarray:
     w = _f32(w).reshape(-1)
     out = np.empty_like(w)

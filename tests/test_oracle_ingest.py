@@ -71,3 +71,22 @@ def test_q4k_unpack_recovers_encoded_values(rows, cols):
     exp_min = dmin.astype(np.float32)[:, :, None] * mn.astype(np.float32)
     assert np.array_equal(scale, exp_scale.reshape(rows, -1).view(np.uint16))
     assert np.array_equal(mins, exp_min.reshape(rows, -1))
+
+
+def test_q4s_dequant_with_zero_mins_is_the_u4_dequant():
+    """With every min 0 the scale-and-min form is the U4 form with zero
+    points 0 at group 32: oracle.q4s_dequant equals oracle.u4_dequant (pinned
+    bit-exact against the reference) bit for bit; a constant min m then
+    subtracts m after the product, rounding once more."""
+    rng = np.random.default_rng(5)
+    n, k = 7, 256
+    codes = rng.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    scale = (rng.standard_normal((n, k // 32)) * 0.02).astype(np.float16).view(np.uint16)
+    zero_m = np.zeros((n, k // 32), np.float32)
+    zp = np.zeros((n * (k // 32) + 1) // 2, np.uint8)
+    w0 = oracle.q4s_dequant(codes, scale, zero_m, n, k)
+    u4 = oracle.u4_dequant(codes, scale, zp, n, k, group=32)
+    assert np.array_equal(w0.view(np.uint32), u4.reshape(n, k).view(np.uint32))
+    m = np.float32(0.0123)
+    w1 = oracle.q4s_dequant(codes, scale, np.full((n, k // 32), m, np.float32), n, k)
+    assert np.array_equal(w1, (u4.reshape(n, k) - m).astype(np.float32))

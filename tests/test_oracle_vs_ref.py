@@ -133,3 +133,23 @@ def test_q4k_unpack_matches_reference_decode(ref, tmp_path):
     assert rebuilt.dtype == np.float32
     assert np.array_equal(rebuilt.view(np.uint32), vals.view(np.uint32))
     assert np.array_equal(s16, s32.astype(np.float16).view(np.uint16))
+
+
+def test_q4s_dequant_matches_reference_decode_when_scale_is_f16_exact(ref, tmp_path):
+    """oracle.q4s_dequant (the scale-and-min form the Q4_K-derived matvec
+    consumes) against the reference's decode_q4_k_block: with d a power of
+    two and the 6-bit scales small, d * sc is exact in f16, so the prepacked
+    f16 scale loses nothing and every dequantized value equals the
+    reference's d1 * q - m1 bit for bit."""
+    rng = np.random.default_rng(21)
+    rows, cols = 16, 512
+    raw = rng.integers(0, 256, (rows, cols // 256, 144), dtype=np.uint8)
+    d = np.ldexp(1.0, rng.integers(-12, -2, rows * 2)) * rng.choice([-1.0, 1.0], rows * 2)
+    dm = rng.uniform(-0.25, 0.25, rows * 2)
+    raw[:, :, 0:2] = d.astype(np.float16).view(np.uint8).reshape(rows, 2, 2)
+    raw[:, :, 2:4] = dm.astype(np.float16).view(np.uint8).reshape(rows, 2, 2)
+    vals = ref.decode_q4k_rows(raw, rows, cols, str(tmp_path / "q4s.gguf"))
+    codes, s16, mins, s32 = oracle.q4k_unpack(raw, rows, cols, f32_scale=True)
+    assert np.array_equal(oracle.half_to_float(s16).reshape(s32.shape), s32)  # the precondition
+    w = oracle.q4s_dequant(codes, s16, mins, rows, cols)
+    assert np.array_equal(w.view(np.uint32), vals.view(np.uint32))
