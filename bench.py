@@ -234,13 +234,28 @@ def profiled_traffic(kernel):
 
 
 def _cpu_model():
+    """The host CPU as /proc/cpuinfo names it: model name (virtualized hosts
+    may report only the family name), x86 family / model / stepping, the
+    widest vector extension and the logical CPU count."""
+    fields = {}
+    n = 0
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" not in line:
+                continue
+            key, val = (t.strip() for t in line.split(":", 1))
+            if key == "processor":
+                n += 1
+            if key in ("model name", "cpu family", "model", "stepping", "flags") and \
+                    key not in fields:
+                fields[key] = val
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    flags = fields.get("flags", "").split()
+    vec = next((f for f in ("avx512f", "avx2", "avx") if f in flags), "none")
+    return (f"{fields.get('model name', 'unknown')} (family {fields.get('cpu family', '?')} "
+            f"model {fields.get('model', '?')} stepping {fields.get('stepping', '?')}, "
+            f"{vec}, {n} logical CPUs)")
 
 
 def main():
