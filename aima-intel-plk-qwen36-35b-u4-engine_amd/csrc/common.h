@@ -399,6 +399,75 @@ __device__ __forceinline__ void rmsnorm_row(const uint16_t* __restrict__ x,
   }
 }
 
+// Router selection for one token by one wave (all 64 lanes active):
+// softmax over `experts` logits in f64 (max and sum by xor shuffles), top-k
+// by (probability desc, id asc) on the f32 probabilities, then the picks
+// renormalized by max(sum, min_weight_sum) summed in rank order.  Lane r < k
+// returns pick r: its id, normalized weight and probability.  PER = logits
+// per lane (experts <= 64 PER).  The select_router_topk semantics
+// (gguf_loader.hpp:371-373).
+template <int PER>
+__device__ __forceinline__ void router_select_wave(const float* __restrict__ l, int experts, int k,
+                                                   float min_weight_sum, int& out_id,
+                                                   float& out_w, float& out_p) {
+  const int lane = threadIdx.x & 63;
+  float v[PER];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = lane + 64 * j;
+    v[j] = i < experts ? l[i] : -INFINITY;
+    mx = fmaxf(mx, v[j]);
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  double e[PER];
+  double sum = 0.0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = lane + 64 * j;
+    e[j] = i < experts ? exp((double)v[j] - (double)mx) : 0.0;
+    sum += e[j];
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+  float p[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int i = lane + 64 * j;
+    p[j] = i < experts ? (float)(e[j] / sum) : -INFINITY;
+  }
+  float my_p = 0.f;
+  int my_i = 0;
+  for (int r = 0; r < k; ++r) {
+    float bp = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int i = lane + 64 * j;
+      if (i < experts && (p[j] > bp || (p[j] == bp && i < bi))) {
+        bp = p[j];
+        bi = i;
+      }
+    }
+    wave_best_pair(bp, bi);
+    if (lane == r) {
+      my_p = bp;
+      my_i = bi;
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      if (lane + 64 * j == bi) p[j] = -INFINITY;
+    }
+  }
+  float s = 0.f;
+  for (int r = 0; r < k; ++r) s += __shfl(my_p, r, 64);
+  const float den = s > min_weight_sum ? s : min_weight_sum;
+  out_id = my_i;
+  out_w = my_p / den;
+  out_p = my_p;
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float s = g >= 0.f ? 1.f / (1.f + expf(-g)) : expf(g) / (1.f + expf(g));
   return g * s * u;

@@ -99,11 +99,24 @@ __device__ __forceinline__ void load_chunks(const uint16_t* __restrict__ x, int 
 // ---------------------------------------------------------------------------
 // phase A
 // ---------------------------------------------------------------------------
-template <int KCH>
+// Routing from the layer's router logits (RPER > 0, the routed stack): every
+// block selects the top-k itself (router_select_wave, wave 0) before it
+// needs its expert id, and block 0 writes the selection to ids_out / w_out
+// for the down kernel and the caller.  This replaces a separate selection
+// launch; the ids and weights are those of aima_router_topk.
+struct RouteIn {
+  const float* logits;  // [experts] (RPER > 0)
+  float min_weight_sum;
+  int32_t* ids_out;     // [k]
+  float* w_out;         // [k]
+};
+
+template <int KCH, int RPER>
 __global__ __launch_bounds__(256) void decode_gateup_kernel(
-    const uint16_t* __restrict__ x, aima_moe_layer L, const int32_t* __restrict__ ids,
+    const uint16_t* __restrict__ x, aima_moe_layer L, const int32_t* __restrict__ ids_in,
     int k, uint32_t* __restrict__ err, uint16_t* __restrict__ act,
-    float* __restrict__ sigma, float* __restrict__ gu_trace, float* __restrict__ gate_logit) {
+    float* __restrict__ sigma, float* __restrict__ gu_trace, float* __restrict__ gate_logit,
+    RouteIn route) {
   using G = Geom<KCH>;
   constexpr int NR = 2 * kPairsPerWave;          // rows per wave
   constexpr int PASSES = (NR + G::RPI - 1) / G::RPI;
@@ -111,8 +124,8 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
   constexpr int kMaxGroups = G::K / 32;
   // the block's scales and zero points: gate rows j0.. and up rows I+j0..,
   // each a contiguous run, staged through LDS (one element per thread)
-  __shared__ uint16_t s_lds[2 * BP * kMaxGroups];
-  __shared__ uint8_t z_lds[2][BP * kMaxGroups / 2];
+  __shared__ __attribute__((aligned(16))) uint16_t s_lds[2 * BP * kMaxGroups];
+  __shared__ __attribute__((aligned(16))) uint8_t z_lds[2][BP * kMaxGroups / 2];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int seg = lane / G::SEG;
@@ -124,6 +137,24 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
   const int64_t pair0 = bpair0 + wave * kPairsPerWave;
   const uint32_t magic = u4_magic();
 
+  const int32_t* ids = ids_in;
+  if constexpr (RPER > 0) {
+    __shared__ int32_t s_ids[16];
+    if (wave == 0) {
+      int pick;
+      float w, p;
+      router_select_wave<RPER>(route.logits, L.experts, k, route.min_weight_sum, pick, w, p);
+      if (lane < k) {
+        s_ids[lane] = pick;
+        if (blockIdx.x == 0) {
+          route.ids_out[lane] = pick;
+          route.w_out[lane] = w;
+        }
+      }
+    }
+    __syncthreads();
+    ids = s_ids;
+  }
   // the block's slot (inter is a multiple of BP: every block lies in one slot)
   const int64_t slot = bpair0 / I;
   const int64_t j0 = bpair0 - slot * I;
@@ -152,32 +183,82 @@ __global__ __launch_bounds__(256) void decode_gateup_kernel(
       zp[h] = V.z[h] + ((r0 * groups) >> 1);  // r0 * groups is even (j0 % 8 == 0)
     }
   }
-  // weights first: they stream while the activation operands are built
+  // Load order: the block's scale and zero-point runs (32-bit words where
+  // aligned), the activations, then the weights, nothing waited for in
+  // between: loads complete in order, so staging the runs in LDS and
+  // building the activation operands wait only for the small early loads
+  // while the weights stream.  An invalid block loads expert 0's rows (in
+  // bounds) and discards them.
+  const int n = BP * groups;  // scales per run (zero points: n / 2 bytes)
+  const int tid = threadIdx.x;
+  const bool words = ((reinterpret_cast<uintptr_t>(sc[0]) | reinterpret_cast<uintptr_t>(sc[1]) |
+                       reinterpret_cast<uintptr_t>(zp[0]) | reinterpret_cast<uintptr_t>(zp[1])) &
+                      3u) == 0;
+  constexpr int kSW = (BP * kMaxGroups + 255) / 256;       // scale words of both runs
+  constexpr int kZW = (BP * kMaxGroups / 4 + 255) / 256;   // zero-point words of both runs
+  uint32_t sw[kSW], zw[kZW];
+#pragma unroll
+  for (int j = 0; j < kSW; ++j) {
+    const int d = tid + 256 * j, h = d >= n / 2;
+    sw[j] = (words && d < n) ? reinterpret_cast<const uint32_t*>(sc[h])[d - h * (n / 2)] : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < kZW; ++j) {
+    const int d = tid + 256 * j, h = d >= n / 8;
+    zw[j] = (words && d < n / 4) ? reinterpret_cast<const uint32_t*>(zp[h])[d - h * (n / 8)] : 0u;
+  }
+  u32x4 xr[G::NC][4];
+#pragma unroll
+  for (int i = 0; i < G::NC; ++i) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(x + (int64_t)(cl + i * G::SEG) * 32);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xr[i][q] = p[q];
+  }
   u32x4 w[PASSES][G::NC];
 #pragma unroll
   for (int ps = 0; ps < PASSES; ++ps) {
     const int ri = ps * G::RPI + seg;  // row index in this wave's list
-    const int64_t row = wave * kPairsPerWave + ri / 2;  // within the block's run
+    const int64_t row = ri < NR ? wave * kPairsPerWave + ri / 2 : 0;  // within the block's run
 #pragma unroll
     for (int i = 0; i < G::NC; ++i) {
       const int c = cl + i * G::SEG;
-      w[ps][i] = (valid && ri < NR) ? load16_nt(qw[ri & 1] + row * (G::K / 2) + (int64_t)c * 16)
-                                    : u32x4{0u, 0u, 0u, 0u};
+      w[ps][i] = load16_nt(qw[ri & 1] + row * (G::K / 2) + (int64_t)c * 16);
     }
   }
-  if (valid) {
-    const int n = BP * groups;  // scales per run
-    for (int t = threadIdx.x; t < 2 * n; t += 256) {
+  if (words) {
+#pragma unroll
+    for (int j = 0; j < kSW; ++j) {
+      const int d = tid + 256 * j;
+      if (d < n) reinterpret_cast<uint32_t*>(s_lds)[d] = sw[j];
+    }
+#pragma unroll
+    for (int j = 0; j < kZW; ++j) {
+      const int d = tid + 256 * j, h = d >= n / 8;
+      if (d < n / 4) reinterpret_cast<uint32_t*>(z_lds[h])[d - h * (n / 8)] = zw[j];
+    }
+  } else {
+    for (int t = tid; t < 2 * n; t += 256) {
       const int up = t >= n;
       s_lds[t] = sc[up][t - up * n];
     }
-    for (int t = threadIdx.x; t < n; t += 256) {
+    for (int t = tid; t < n; t += 256) {
       const int up = t >= n / 2;
       z_lds[up][t - up * (n / 2)] = zp[up][t - up * (n / 2)];
     }
   }
   XChunk xc[G::NC];
-  load_chunks<KCH>(x, cl, xc);
+#pragma unroll
+  for (int i = 0; i < G::NC; ++i) {
+    uint32_t xw[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      xw[4 * q + 0] = xr[i][q][0];
+      xw[4 * q + 1] = xr[i][q][1];
+      xw[4 * q + 2] = xr[i][q][2];
+      xw[4 * q + 3] = xr[i][q][3];
+    }
+    make_xchunk(xw, xc[i]);
+  }
   __syncthreads();
   float s[PASSES][G::NC];
   uint32_t z[PASSES][G::NC];
@@ -395,14 +476,37 @@ struct DecodeTrace {
   float* down;        // [(k+1)][H]
 };
 
-template <int KCH>
-static void launch_gateup(const uint16_t* x, const aima_moe_layer& L, const int32_t* ids, int k,
-                          const DecodeWs& w, const DecodeTrace& tr, hipStream_t st) {
+template <int KCH, int RPER>
+static void launch_gateup_r(const uint16_t* x, const aima_moe_layer& L, const int32_t* ids, int k,
+                            const DecodeWs& w, const DecodeTrace& tr, const RouteIn& route,
+                            hipStream_t st) {
   const int64_t pairs = (int64_t)(k + 1) * L.inter;
   const int64_t waves = (pairs + kPairsPerWave - 1) / kPairsPerWave;
   const int64_t blocks = (waves + 3) / 4;
-  hipLaunchKernelGGL((decode_gateup_kernel<KCH>), dim3((unsigned)blocks), dim3(256), 0, st, x, L,
-                     ids, k, w.err, w.act, w.sigma, tr.gate_up, tr.gate_logit);
+  hipLaunchKernelGGL((decode_gateup_kernel<KCH, RPER>), dim3((unsigned)blocks), dim3(256), 0, st,
+                     x, L, ids, k, w.err, w.act, w.sigma, tr.gate_up, tr.gate_logit, route);
+}
+
+// route.logits null: the ids are given; else the selection per block, with
+// the logits per lane (experts / 64 rounded up to a power of two) as the
+// template argument.
+template <int KCH>
+static void launch_gateup(const uint16_t* x, const aima_moe_layer& L, const int32_t* ids, int k,
+                          const DecodeWs& w, const DecodeTrace& tr, hipStream_t st,
+                          const RouteIn& route = RouteIn{}) {
+  if (!route.logits) {
+    launch_gateup_r<KCH, 0>(x, L, ids, k, w, tr, route, st);
+  } else if (L.experts <= 64) {
+    launch_gateup_r<KCH, 1>(x, L, ids, k, w, tr, route, st);
+  } else if (L.experts <= 128) {
+    launch_gateup_r<KCH, 2>(x, L, ids, k, w, tr, route, st);
+  } else if (L.experts <= 256) {
+    launch_gateup_r<KCH, 4>(x, L, ids, k, w, tr, route, st);
+  } else if (L.experts <= 512) {
+    launch_gateup_r<KCH, 8>(x, L, ids, k, w, tr, route, st);
+  } else {
+    launch_gateup_r<KCH, 16>(x, L, ids, k, w, tr, route, st);
+  }
 }
 
 template <int KCH>
@@ -414,14 +518,18 @@ static void launch_down(const aima_moe_layer& L, const int32_t* ids, const float
                      ids, rw, k, w.act, w.sigma, residual, out, tr.down);
 }
 
+// route.logits set: the gate/up kernel selects the route from the logits
+// and writes it to ids / rw (route.ids_out == ids, route.w_out == rw), which
+// the down kernel then reads.
 static int decode_layer(const aima_moe_layer& L, const uint16_t* x, const uint16_t* residual,
                         const int32_t* ids, const float* rw, int k, uint16_t* out,
-                        const DecodeWs& w, hipStream_t st, const DecodeTrace& tr = DecodeTrace{}) {
+                        const DecodeWs& w, hipStream_t st, const DecodeTrace& tr = DecodeTrace{},
+                        const RouteIn& route = RouteIn{}) {
   switch (L.hidden / 32) {
-    case 16: launch_gateup<16>(x, L, ids, k, w, tr, st); break;
-    case 32: launch_gateup<32>(x, L, ids, k, w, tr, st); break;
-    case 64: launch_gateup<64>(x, L, ids, k, w, tr, st); break;
-    case 128: launch_gateup<128>(x, L, ids, k, w, tr, st); break;
+    case 16: launch_gateup<16>(x, L, ids, k, w, tr, st, route); break;
+    case 32: launch_gateup<32>(x, L, ids, k, w, tr, st, route); break;
+    case 64: launch_gateup<64>(x, L, ids, k, w, tr, st, route); break;
+    case 128: launch_gateup<128>(x, L, ids, k, w, tr, st, route); break;
     default: return fail(AIMA_E_UNSUPPORTED, "moe decode: unsupported hidden size");
   }
   int rc = launch_check("moe decode gate/up");
@@ -713,10 +821,14 @@ static int routed_stack_run(const aima_moe_layer* layers, const aima_u4_tensor* 
     if (rc != AIMA_OK) return rc;
     int32_t* ids_l = ids + (int64_t)l * k;
     float* w_l = weights + (int64_t)l * k;
-    rc = router_topk_launch(w.logits, 1, L.experts, k, min_weight_sum, ids_l, w_l, st);
-    if (rc != AIMA_OK) return rc;
     uint16_t* dst = (l == n_layers - 1) ? out : w.r[l & 1];
-    rc = decode_layer(L, w.h, r, ids_l, w_l, k, dst, w, st);
+    // the selection runs inside the gate/up kernel (no separate launch)
+    RouteIn route;
+    route.logits = w.logits;
+    route.min_weight_sum = min_weight_sum;
+    route.ids_out = ids_l;
+    route.w_out = w_l;
+    rc = decode_layer(L, w.h, r, ids_l, w_l, k, dst, w, st, DecodeTrace{}, route);
     if (rc != AIMA_OK) return rc;
     r = dst;
   }

@@ -414,63 +414,13 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   const int lane = threadIdx.x & 63;
   const int64_t token = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (token >= tokens) return;
-  const float* l = logits + token * experts;
-  float v[PER];
-  float mx = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = lane + 64 * j;
-    v[j] = i < experts ? l[i] : -INFINITY;
-    mx = fmaxf(mx, v[j]);
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  double e[PER];
-  double sum = 0.0;
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = lane + 64 * j;
-    e[j] = i < experts ? exp((double)v[j] - (double)mx) : 0.0;
-    sum += e[j];
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-  float p[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    const int i = lane + 64 * j;
-    p[j] = i < experts ? (float)(e[j] / sum) : -INFINITY;
-  }
-  float my_p = 0.f;
-  int my_i = 0;
-  for (int r = 0; r < k; ++r) {
-    float bp = -INFINITY;
-    int bi = 0x7fffffff;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int i = lane + 64 * j;
-      if (i < experts && (p[j] > bp || (p[j] == bp && i < bi))) {
-        bp = p[j];
-        bi = i;
-      }
-    }
-    wave_best_pair(bp, bi);
-    if (lane == r) {
-      my_p = bp;
-      my_i = bi;
-    }
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      if (lane + 64 * j == bi) p[j] = -INFINITY;
-    }
-  }
-  float s = 0.f;
-  for (int r = 0; r < k; ++r) s += __shfl(my_p, r, 64);
-  const float den = s > min_weight_sum ? s : min_weight_sum;
+  int pick;
+  float w, p;
+  router_select_wave<PER>(logits + token * experts, experts, k, min_weight_sum, pick, w, p);
   if (lane < k) {
-    ids[token * k + lane] = my_i;
-    weights[token * k + lane] = my_p / den;
-    if (probs) probs[token * k + lane] = my_p;  // the picks' softmax probabilities
+    ids[token * k + lane] = pick;
+    weights[token * k + lane] = w;
+    if (probs) probs[token * k + lane] = p;  // the picks' softmax probabilities
   }
 }
 
