@@ -13,6 +13,7 @@ from .layout import MoeLayerWeights, U4Weight  # noqa: F401
 from .ops import (  # noqa: F401
     MIN_WEIGHT_SUM,
     DecodePlan,
+    DecodeRoutes,
     Qwen36MoeFfnLayerResult,
     RouterTopKSelection,
     Workspace,

@@ -125,6 +125,8 @@ SIGNATURES = {
     "aima_workspace_error": (C.c_int, [_vp, C.POINTER(C.c_uint32), _vp]),
     "aima_moe_decode_plan_create": (C.c_int, [_LP, _i32, _i32, C.POINTER(_vp)]),
     "aima_moe_decode_plan_run": (C.c_int, [_vp, _f32, _vp, _vp, _vp, _vp, _f32, _vp, _vp]),
+    "aima_moe_decode_plan_set_routers": (C.c_int, [_vp, C.POINTER(U4TensorC)]),
+    "aima_moe_decode_plan_run_routed": (C.c_int, [_vp, _f32, _vp, _f32, _vp, _vp, _vp, _vp, _vp]),
     "aima_moe_decode_plan_error": (C.c_int, [_vp, C.POINTER(C.c_uint32), _vp]),
     "aima_moe_decode_plan_destroy": (C.c_int, [_vp]),
 }

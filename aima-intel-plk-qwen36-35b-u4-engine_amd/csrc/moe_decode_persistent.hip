@@ -77,6 +77,7 @@ constexpr int kChunksB = kXcdPairs / 32;                 // 18 B-phase operand c
 constexpr int kMaxK = 8;
 constexpr uint32_t kSpinLimit = 1u << 22;
 constexpr int kMaxLayers = 79;
+constexpr int kRouterRows = kPerXcd * kWaves;            // 256: router rows per XCD (routed plan)
 static_assert(kPairs % 3 == 0, "blocks own whole act records");
 static_assert(kActRecords <= 192, "the activation poll covers records 0..191");
 static_assert(kRowsB % kWaves == 0 && kWaveRowsB == 8, "8 output rows per wave");
@@ -88,12 +89,12 @@ static_assert(kRowsB % kWaves == 0 && kWaveRowsB == 8, "8 output rows per wave")
 // form two tensors), the shared expert's gate/up at unit 0, both down
 // projections, the shared gate vector and the RMSNorm weight.
 struct PlanLayer {
-  const uint8_t* gq[2];
-  const uint16_t* gs[2];
-  const uint8_t* gz[2];
-  const uint8_t* sq[2];
-  const uint16_t* ss[2];
-  const uint8_t* sz[2];
+  const uint8_t *gq0, *gq1;  // (named fields, no arrays: a register copy of
+  const uint16_t *gs0, *gs1;  // an entry is then never indexed at run time)
+  const uint8_t *gz0, *gz1;
+  const uint8_t *sq0, *sq1;
+  const uint16_t *ss0, *ss1;
+  const uint8_t *sz0, *sz1;
   const uint8_t* dq;
   const uint16_t* ds;
   const uint8_t* dz;
@@ -102,6 +103,9 @@ struct PlanLayer {
   const uint8_t* sdz;
   const uint16_t* gate_vec;
   const float* norm;
+  const uint8_t* rq;              // router [experts][kH] (routed plan; else null)
+  const uint16_t* rs;
+  const uint8_t* rz;
   uint32_t estride_q, estride_s, estride_z;  // routed gate/up bytes per expert
   uint32_t pad;
 };
@@ -125,6 +129,10 @@ struct PersistArgs {
   uint64_t* pbuf;                 // [2][xcd][H]            {f32, epoch}
   uint32_t* route_ids;            // [L][k]                 {id, epoch}
   uint64_t* route_w;              // [L][k]                 {f32, epoch}
+  uint64_t* lgx;                  // [xcd][2][kRouterRows]  {f32, epoch}, XCD-local
+  float* logits_out;              // routed plan: [L][E] or null
+  int32_t* ids_out;               // routed plan: [L][k] or null
+  float* w_out;                   // routed plan: [L][k] or null
   uint32_t* epoch_counter;
   uint32_t* err;
 };
@@ -184,6 +192,20 @@ __device__ __forceinline__ void poll8(const void* p, int stride, uint64_t (&v)[8
       : "memory");
 }
 
+// four 8-byte loads `stride` bytes apart
+__device__ __forceinline__ void poll4(const void* p, int stride, uint64_t (&v)[4]) {
+  const char* c = reinterpret_cast<const char*>(p);
+  asm volatile(
+      "global_load_dwordx2 %0, %4, off sc1\n\t"
+      "global_load_dwordx2 %1, %5, off sc1\n\t"
+      "global_load_dwordx2 %2, %6, off sc1\n\t"
+      "global_load_dwordx2 %3, %7, off sc1\n\t"
+      "s_waitcnt vmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "v"(c), "v"(c + stride), "v"(c + 2 * stride), "v"(c + 3 * stride)
+      : "memory");
+}
+
 __device__ __forceinline__ uint32_t pack_word(uint16_t v, uint32_t epoch) {
   return (uint32_t)v | (epoch << 16);
 }
@@ -208,6 +230,8 @@ struct SharedState {
   float route_w[kMaxLayers][kMaxK];
   float sigma;
   int abort;
+  int reroute;                         // routed plan: the layer's route changed
+  int32_t rank[kMaxK + 1];             // routed plan: ranks 0..k by logit
 };
 
 // Router top-k for one layer (one wave): f64 softmax over the logits,
@@ -305,6 +329,226 @@ __device__ void route_layer(const float* __restrict__ l, int E, int k, float min
   if (lane < k) w[0] = w[0] / den;
 }
 
+// Router top-k of one layer for the routed plan (experts <= 256; lane l of
+// a wave holds the logits of experts l + 64 t).  The rule is
+// select_router_topk's (gguf_loader.hpp:371-373): softmax in f64, the top k
+// by (probability desc, id asc) on the f32 probabilities, the picks
+// renormalized by max(rank-order sum, min_sum).
+//
+// The probabilities are a non-decreasing function of the logits, so ranking
+// the logits almost always gives the answer, and the ranking needs no
+// exponentials: rank_logits (one wave) ranks 32-bit keys made of the top 24
+// bits of the logit's order-preserving image and the complemented id, one
+// wave maximum per rank, while another wave computes the probabilities
+// (softmax_probs).  The layer's weight loads start from the ranking;
+// route_confirm then checks it exactly: if the probabilities of ranks 0..k
+// decrease strictly and exactly k + 1 probabilities are >= that of rank k,
+// then every other probability is below rank k's, so ranks 0..k-1 are the k
+// largest probabilities in order, and the route stands.  Otherwise (equal or
+// nearly equal logits, rare) select_probs ranks the probabilities themselves
+// and the loads are issued again.
+__device__ __forceinline__ uint64_t u64_of(uint32_t lo, uint32_t hi) {
+  return ((uint64_t)hi << 32) | lo;
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  return u64_of(dpp_u32<CTRL>((uint32_t)v), dpp_u32<CTRL>((uint32_t)(v >> 32)));
+}
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t v, int l) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, l);
+}
+__device__ __forceinline__ uint64_t readlane_u64(uint64_t v, int l) {
+  return u64_of(readlane_u32((uint32_t)v, l), readlane_u32((uint32_t)(v >> 32), l));
+}
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// Wave reductions: DPP inside 16-lane rows (quad_perm [1,0,3,2], [2,3,0,1],
+// row_half_mirror, row_mirror), then across rows, so every lane gets the same
+// value.  The u32 forms cross rows with row_bcast:15 (rows 1 and 3 take the
+// last lane of the row below) and row_bcast:31 (rows 2 and 3 take lane 31),
+// which leaves the total in lane 63; the others read the four rows in a
+// fixed order.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_rows_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, ROWS, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<0xB1>(v));
+  v = max(v, dpp_u32<0x4E>(v));
+  v = max(v, dpp_u32<0x141>(v));
+  v = max(v, dpp_u32<0x140>(v));
+  v = max(v, dpp_rows_u32<0x142, 0xA>(v));
+  v = max(v, dpp_rows_u32<0x143, 0xC>(v));
+  return readlane_u32(v, 63);
+}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+  v = max_u64(v, dpp_u64<0xB1>(v));
+  v = max_u64(v, dpp_u64<0x4E>(v));
+  v = max_u64(v, dpp_u64<0x141>(v));
+  v = max_u64(v, dpp_u64<0x140>(v));
+  return max_u64(max_u64(readlane_u64(v, 0), readlane_u64(v, 16)),
+                 max_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  return __builtin_bit_cast(double, dpp_u64<CTRL>(__builtin_bit_cast(uint64_t, v)));
+}
+__device__ __forceinline__ double readlane_f64(double v, int l) {
+  return __builtin_bit_cast(double, readlane_u64(__builtin_bit_cast(uint64_t, v), l));
+}
+__device__ __forceinline__ double wave_sum_f64(double v) {
+  v += dpp_f64<0xB1>(v);
+  v += dpp_f64<0x4E>(v);
+  v += dpp_f64<0x141>(v);
+  v += dpp_f64<0x140>(v);
+  return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
+}
+
+// Lane r <= k returns the expert id of rank r by the 32-bit key (-1 past
+// the finite logits).  A lane keeps its four keys sorted; a round is one
+// wave maximum of the lanes' heads (keys are unique: the low byte is the
+// complemented id) and the winning lane dropping its head.
+__device__ int rank_logits(const float (&v)[4], int experts, int k) {
+  const int lane = threadIdx.x & 63;
+  uint32_t q[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int i = lane + 64 * t;
+    const uint32_t b = __builtin_bit_cast(uint32_t, v[t]);
+    const uint32_t m = (b & 0x80000000u) ? ~b : (b | 0x80000000u);  // order-preserving
+    // NaN and ids past the experts are never ranked; every finite logit
+    // keeps a nonzero key (-inf maps to 0x007fffff)
+    q[t] = (i < experts && v[t] == v[t]) ? ((m & 0xffffff00u) | (uint32_t)(255 - i)) : 0u;
+  }
+  auto cx = [&](int x, int y) {
+    const uint32_t hi = max(q[x], q[y]), lo = min(q[x], q[y]);
+    q[x] = hi;
+    q[y] = lo;
+  };
+  cx(0, 1);
+  cx(2, 3);
+  cx(0, 2);
+  cx(1, 3);
+  cx(1, 2);
+  int mine = -1;
+  for (int r = 0; r <= k; ++r) {
+    const uint32_t m = wave_max_u32(q[0]);
+    if (lane == r) mine = m == 0 ? -1 : 255 - (int)(m & 0xffu);
+    const bool pop = q[0] == m;
+    q[0] = pop ? q[1] : q[0];
+    q[1] = pop ? q[2] : q[1];
+    q[2] = pop ? q[3] : q[2];
+    q[3] = pop ? 0u : q[3];
+  }
+  return mine;
+}
+
+// f32 probabilities of the softmax (f64 exp and sum); -inf past `experts`
+__device__ void softmax_probs(const float (&v)[4], int experts, float (&p)[4]) {
+  const int lane = threadIdx.x & 63;
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    if (lane + 64 * t < experts) mx = fmaxf(mx, v[t]);
+  }
+  mx = fmaxf(mx, dpp_mov<0xB1>(mx));
+  mx = fmaxf(mx, dpp_mov<0x4E>(mx));
+  mx = fmaxf(mx, dpp_mov<0x141>(mx));
+  mx = fmaxf(mx, dpp_mov<0x140>(mx));
+  mx = fmaxf(fmaxf(lane_read(mx, 0), lane_read(mx, 16)), fmaxf(lane_read(mx, 32), lane_read(mx, 48)));
+  double e[4];
+  double sum = 0.0;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    e[t] = lane + 64 * t < experts ? exp((double)v[t] - (double)mx) : 0.0;
+    sum += e[t];
+  }
+  sum = wave_sum_f64(sum);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) p[t] = lane + 64 * t < experts ? (float)(e[t] / sum) : -INFINITY;
+}
+
+// Lane r < k: weight of rank r given the rank-order probabilities pr.
+__device__ __forceinline__ float rank_weight(float pr, int k, float min_sum) {
+  float psum = 0.f;
+  for (int r = 0; r < k; ++r) {
+    const float x = lane_read(pr, r);
+    psum = r == 0 ? x : psum + x;  // sequential f32 sum in rank order
+  }
+  return pr / (psum > min_sum ? psum : min_sum);
+}
+
+// The ranking of the probabilities themselves: 64-bit keys, probability
+// bits (p >= 0, so they order like the values) above the complemented id.
+// Lane r < k returns rank r's id (-1 when no finite probability is left)
+// and weight.
+__device__ void select_probs(const float (&p)[4], int experts, int k, float min_sum,
+                             int& out_id, float& out_w) {
+  const int lane = threadIdx.x & 63;
+  uint64_t q[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int i = lane + 64 * t;
+    q[t] = (i < experts && p[t] == p[t]) ? u64_of(~(uint32_t)i, __builtin_bit_cast(uint32_t, p[t]))
+                                         : 0;
+  }
+  auto cx = [](uint64_t& a, uint64_t& b) {
+    const uint64_t h = max_u64(a, b);
+    b = a > b ? b : a;
+    a = h;
+  };
+  cx(q[0], q[1]);
+  cx(q[2], q[3]);
+  cx(q[0], q[2]);
+  cx(q[1], q[3]);
+  cx(q[1], q[2]);
+  uint64_t mine = 0;
+  for (int r = 0; r < k; ++r) {
+    const uint64_t m = wave_max_u64(q[0]);
+    if (lane == r) mine = m;
+    const bool pop = q[0] == m;
+    q[0] = pop ? q[1] : q[0];
+    q[1] = pop ? q[2] : q[1];
+    q[2] = pop ? q[3] : q[2];
+    q[3] = pop ? 0 : q[3];
+  }
+  out_id = mine == 0 ? -1 : (int)~(uint32_t)mine;
+  out_w = rank_weight(__builtin_bit_cast(float, (uint32_t)(mine >> 32)), k, min_sum);
+}
+
+// Confirms the ranking `rank_id` (lane r <= k; -1 where no finite logit was
+// left) against the probabilities p: true when they decrease strictly over
+// ranks 0..k and no probability outside those ranks reaches rank k's, with
+// lane r < k's weight in out_w.
+__device__ bool route_confirm(const float (&p)[4], int experts, int rank_id, int k,
+                              float min_sum, float& out_w) {
+  const int lane = threadIdx.x & 63;
+  const int src = rank_id & 63, t = rank_id >> 6;
+  float pr = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const float x = __shfl(p[u], src, 64);
+    if (rank_id >= 0 && t == u) pr = x;
+  }
+  const float next = __shfl(pr, lane + 1, 64);
+  const uint64_t mask = (1ull << k) - 1ull;
+  bool ok = (__ballot(lane < k && pr > next) & mask) == mask;
+  const int last = __shfl(rank_id, k, 64);
+  if (last >= 0) {
+    // exactly ranks 0..k at or above rank k's probability
+    const float pk = __shfl(pr, k, 64);
+    int n = 0;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) n += __popcll(__ballot(lane + 64 * u < experts && p[u] >= pk));
+    ok = ok && n == k + 1;
+  }
+  out_w = rank_weight(pr, k, min_sum);
+  return ok;
+}
+
 __device__ __forceinline__ uint32_t h2bits(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
 
 // XChunk <-> LDS (word-group major arrays indexed by chunk)
@@ -375,7 +619,14 @@ __device__ uint64_t* g_trace = nullptr;
 
 // G128: specialized for 128-wide quantization groups (gathered scale and
 // zero-point loads); the other instance serves every supported group size.
-template <bool G128>
+// ROUTED: each layer's route comes from its own normalized input (true
+// decode, run_qwen36_moe_ffn_layer's router step, gguf_loader.cpp:5704-5711):
+// after the RMSNorm every XCD computes all router logits itself (wave w of
+// block j takes expert 8j + w, from router rows prefetched a layer ahead),
+// exchanges them XCD-locally, and one wave of every block selects the top-k;
+// only then are the layer's routed gate/up and down rows loaded.  Otherwise
+// the routes of all layers come from the launch's logits or ids.
+template <bool G128, bool ROUTED>
 __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistArgs a) {
   __shared__ SharedState S;
   const int lane = threadIdx.x & 63;
@@ -436,7 +687,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // ---- prologue --------------------------------------------------------------
   // Block L computes and publishes layer L's route (wave 0); then every block
   // reads all routes into LDS (one wave per layer, in parallel).
-  if (wave == 0) {
+  if (!ROUTED && wave == 0) {
     for (int L = b; L < a.n_layers; L += nb) {
       int32_t id = 0;
       float w = 0.f;
@@ -449,7 +700,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     }
   }
   // lane l of wave w reads slot l & 7 of layer L0 + w + 8 (l >> 3)
-  for (int L0 = 0; L0 < a.n_layers; L0 += 8 * kWaves) {
+  for (int L0 = 0; !ROUTED && L0 < a.n_layers; L0 += 8 * kWaves) {
     const int L = L0 + wave + kWaves * (lane >> 3);
     const int s = lane & 7;
     const bool mine = L < a.n_layers && s < k;
@@ -550,10 +801,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // gate/up gather (groups of 128: 16 per row): lanes 0..39 = scale words
   // 0..7 of row slots 0..4, lanes 40..49 = zero-point words 0..1 of row slots
   // 0..4 (lanes above repeat lane 49)
-  auto gather_a = [&](int L) {
+  // The row loaders take the layer's table entry (in LDS) and routed expert.
+  auto gather_a = [&](const PlanLayer& Ly, uint32_t e) {
     const int ln = opaque_v(threadIdx.x & 63);
-    const PlanLayer& Ly = S.table[L];
-    const uint32_t e = slot_expert(L);
     const int q = min(ln, 49);
     const bool is_s = q < 40;
     const int i = is_s ? (q >> 3) : ((q - 40) >> 1);
@@ -563,12 +813,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     const bool routed = p < kI;
     const int unit = routed ? p : x * kSlice + (p - kI);
     const bool up = (ri & 1) != 0;
-    const AIMA_GLOBAL uint8_t* rs0 = uptr(Ly.gs[0]) + (size_t)e * Ly.estride_s;
-    const AIMA_GLOBAL uint8_t* rs1 = uptr(Ly.gs[1]) + (size_t)e * Ly.estride_s;
-    const AIMA_GLOBAL uint8_t* rz0 = uptr(Ly.gz[0]) + (size_t)e * Ly.estride_z;
-    const AIMA_GLOBAL uint8_t* rz1 = uptr(Ly.gz[1]) + (size_t)e * Ly.estride_z;
-    const AIMA_GLOBAL uint8_t* hs = up ? uptr(Ly.ss[1]) : uptr(Ly.ss[0]);
-    const AIMA_GLOBAL uint8_t* hz = up ? uptr(Ly.sz[1]) : uptr(Ly.sz[0]);
+    const AIMA_GLOBAL uint8_t* rs0 = uptr(Ly.gs0) + (size_t)e * Ly.estride_s;
+    const AIMA_GLOBAL uint8_t* rs1 = uptr(Ly.gs1) + (size_t)e * Ly.estride_s;
+    const AIMA_GLOBAL uint8_t* rz0 = uptr(Ly.gz0) + (size_t)e * Ly.estride_z;
+    const AIMA_GLOBAL uint8_t* rz1 = uptr(Ly.gz1) + (size_t)e * Ly.estride_z;
+    const AIMA_GLOBAL uint8_t* hs = up ? uptr(Ly.ss1) : uptr(Ly.ss0);
+    const AIMA_GLOBAL uint8_t* hz = up ? uptr(Ly.sz1) : uptr(Ly.sz0);
     const AIMA_GLOBAL uint8_t* rs = up ? rs1 : rs0;
     const AIMA_GLOBAL uint8_t* rz = up ? rz1 : rz0;
     const AIMA_GLOBAL uint8_t* base = is_s ? (routed ? rs : hs) : (routed ? rz : hz);
@@ -578,10 +828,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // down gather (4 groups per row; the wave's 8 rows are consecutive):
   // lanes 0..15 = routed scale words, 16..19 = routed zero-point words,
   // 20..35 = shared scale words, 36..39 = shared zero-point words
-  auto gather_b = [&](int L) {
+  auto gather_b = [&](const PlanLayer& Ly, uint32_t e) {
     const int ln = opaque_v(threadIdx.x & 63);
-    const PlanLayer& Ly = S.table[L];
-    const uint32_t e = slot_expert(L);
     const uint32_t sbytes = (uint32_t)kH * 4 * 2;
     const uint32_t zbytes = (uint32_t)kH * 4 / 2;
     const uint32_t h0 = (uint32_t)(j * kRowsB + wave * kWaveRowsB);
@@ -602,41 +850,40 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // control duties of wave 0 fall on a wave with four.  prefetch_a1 loads the
   // wave's row slot i, prefetch_a all of them (a surplus slot is clamped onto
   // the block's last row).
-  auto prefetch_a1 = [&](int L, int i) {
+  auto prefetch_a1 = [&](const PlanLayer& Ly, uint32_t e, int i) {
     const int ln = opaque_v(threadIdx.x & 63);
-    const PlanLayer& Ly = S.table[L];
-    const uint32_t e = slot_expert(L);
     const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
     const int h = ri & 1;
     const int p = j * kPairs + (ri >> 1);
     const bool routed = p < kI;
-    const AIMA_GLOBAL uint8_t* w = routed ? uptr(Ly.gq[h]) + (size_t)e * Ly.estride_q
-                                          : uptr(Ly.sq[h]);
-    const AIMA_GLOBAL uint8_t* sp = routed ? uptr(Ly.gs[h]) + (size_t)e * Ly.estride_s
-                                           : uptr(Ly.ss[h]);
-    const AIMA_GLOBAL uint8_t* zp = routed ? uptr(Ly.gz[h]) + (size_t)e * Ly.estride_z
-                                           : uptr(Ly.sz[h]);
+    const AIMA_GLOBAL uint8_t* w =
+        routed ? uptr(h ? Ly.gq1 : Ly.gq0) + (size_t)e * Ly.estride_q
+               : uptr(h ? Ly.sq1 : Ly.sq0);
+    const AIMA_GLOBAL uint8_t* sp =
+        routed ? uptr(h ? Ly.gs1 : Ly.gs0) + (size_t)e * Ly.estride_s
+               : uptr(h ? Ly.ss1 : Ly.ss0);
+    const AIMA_GLOBAL uint8_t* zp =
+        routed ? uptr(h ? Ly.gz1 : Ly.gz0) + (size_t)e * Ly.estride_z
+               : uptr(h ? Ly.sz1 : Ly.sz0);
     const int unit = routed ? p : x * kSlice + (p - kI);
     const int gi = unit * gA + ((ln * 32) >> glog2);
     wa_n[i] = ld_w(w, (uint32_t)unit * (kH / 2) + ln * 16);
     if (g128) {
-      if (i == 0) gather_a(L);
+      if (i == 0) gather_a(Ly, e);
     } else {
       sa_n[i] = ld_u32(sp, (gi * 2) & ~3);
       za_n[i] = ld_u32(zp, (gi >> 1) & ~3);
     }
   };
-  auto prefetch_a = [&](int L) {
+  auto prefetch_a = [&](const PlanLayer& Ly, uint32_t e) {
 #pragma unroll
-    for (int i = 0; i < kMaxRowsA; ++i) prefetch_a1(L, i);
+    for (int i = 0; i < kMaxRowsA; ++i) prefetch_a1(Ly, e, i);
   };
   // down rows: wave w owns block rows 8w .. 8w+7; units 0, 1 = routed rows
   // 4u + (lane >> 4), chunk lane & 15; unit 2 = the shared slice, row
   // (lane & 15) >> 1, chunk 2x + (lane & 1) of the full shared row
-  auto prefetch_b = [&](int L) {
+  auto prefetch_b = [&](const PlanLayer& Ly, uint32_t e) {
     const int ln = opaque_v(threadIdx.x & 63);
-    const PlanLayer& Ly = S.table[L];
-    const uint32_t e = slot_expert(L);
     const uint32_t wbytes = (uint32_t)kH * (kI / 2);
     const uint32_t sbytes = (uint32_t)kH * gB * 2;
     const uint32_t zbytes = (uint32_t)kH * gB / 2;
@@ -665,7 +912,94 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
         zb_n[2] = ld_u32(uptr(Ly.sdz), (gi >> 1) & ~3);
       }
     }
-    if (g128) gather_b(L);
+    if (g128) gather_b(Ly, e);
+  };
+  // All gate/up and down rows of layer L in one burst (routed plan): the
+  // table fields are read first and each row's base chosen by selects, so the
+  // loads leave back to back (the loaders above read the table per row,
+  // which the prefetch interleaved with the dot products can afford; a burst
+  // that starts when the route is known cannot).  Same rows, lanes and
+  // clamping as prefetch_a, gather_a, prefetch_b and gather_b.
+  auto issue_rows = [&](int L) {
+    const int ln = opaque_v(threadIdx.x & 63);
+    const PlanLayer& T = S.table[L];
+    const uint32_t e = slot_expert(L);
+    const uint64_t eq = (uint64_t)e * T.estride_q, es = (uint64_t)e * T.estride_s,
+                   ez = (uint64_t)e * T.estride_z;
+    const AIMA_GLOBAL uint8_t *rq0 = uptr(T.gq0) + eq, *rq1 = uptr(T.gq1) + eq;
+    const AIMA_GLOBAL uint8_t *rs0 = uptr(T.gs0) + es, *rs1 = uptr(T.gs1) + es;
+    const AIMA_GLOBAL uint8_t *rz0 = uptr(T.gz0) + ez, *rz1 = uptr(T.gz1) + ez;
+    const AIMA_GLOBAL uint8_t *hq0 = uptr(T.sq0), *hq1 = uptr(T.sq1);
+    const AIMA_GLOBAL uint8_t *hs0 = uptr(T.ss0), *hs1 = uptr(T.ss1);
+    const AIMA_GLOBAL uint8_t *hz0 = uptr(T.sz0), *hz1 = uptr(T.sz1);
+    const AIMA_GLOBAL uint8_t* dw = uptr(T.dq) + (size_t)e * ((uint32_t)kH * (kI / 2));
+    const AIMA_GLOBAL uint8_t* dsc = uptr(T.ds) + (size_t)e * ((uint32_t)kH * gB * 2);
+    const AIMA_GLOBAL uint8_t* dzp = uptr(T.dz) + (size_t)e * ((uint32_t)kH * gB / 2);
+    const AIMA_GLOBAL uint8_t *sw = uptr(T.sdq), *ssc = uptr(T.sds), *szp = uptr(T.sdz);
+    // gate/up rows
+#pragma unroll
+    for (int i = 0; i < kMaxRowsA; ++i) {
+      const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
+      const bool h = (ri & 1) != 0;
+      const int p = j * kPairs + (ri >> 1);
+      const bool routed = p < kI;
+      const int unit = routed ? p : x * kSlice + (p - kI);
+      wa_n[i] = ld_w(routed ? (h ? rq1 : rq0) : (h ? hq1 : hq0),
+                     (uint32_t)unit * (kH / 2) + ln * 16);
+      if (!g128) {
+        const int gi = unit * gA + ((ln * 32) >> glog2);
+        sa_n[i] = ld_u32(routed ? (h ? rs1 : rs0) : (h ? hs1 : hs0), (gi * 2) & ~3);
+        za_n[i] = ld_u32(routed ? (h ? rz1 : rz0) : (h ? hz1 : hz0), (gi >> 1) & ~3);
+      }
+    }
+    if (g128) {
+      const int q = min(ln, 49);
+      const bool is_s = q < 40;
+      const int i = is_s ? (q >> 3) : ((q - 40) >> 1);
+      const int w = is_s ? (q & 7) : ((q - 40) & 1);
+      const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
+      const int p = j * kPairs + (ri >> 1);
+      const bool routed = p < kI;
+      const int unit = routed ? p : x * kSlice + (p - kI);
+      const bool up = (ri & 1) != 0;
+      const AIMA_GLOBAL uint8_t* base =
+          is_s ? (routed ? (up ? rs1 : rs0) : (up ? hs1 : hs0))
+               : (routed ? (up ? rz1 : rz0) : (up ? hz1 : hz0));
+      const uint32_t off = is_s ? (uint32_t)unit * 32 + 4 * w : (uint32_t)unit * 8 + 4 * w;
+      gsa_n = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
+    }
+    // down rows
+    const int h0 = j * kRowsB + wave * kWaveRowsB;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int row = h0 + 4 * u + (ln >> 4);
+      const int cl = ln & 15;
+      wb_n[u] = ld_w(dw, (uint32_t)row * (kI / 2) + cl * 16);
+      if (!g128) {
+        const int gi = row * gB + ((cl * 32) >> glog2);
+        sb_n[u] = ld_u32(dsc, (gi * 2) & ~3);
+        zb_n[u] = ld_u32(dzp, (gi >> 1) & ~3);
+      }
+    }
+    {
+      const int row = h0 + ((ln & 15) >> 1);
+      const int ch = 2 * x + (ln & 1);
+      wb_n[2] = ld_w(sw, (uint32_t)row * (kI / 2) + ch * 16);
+      if (!g128) {
+        const int gi = row * gB + ((ch * 32) >> glog2);
+        sb_n[2] = ld_u32(ssc, (gi * 2) & ~3);
+        zb_n[2] = ld_u32(szp, (gi >> 1) & ~3);
+      }
+    }
+    if (g128) {
+      const int q = min(ln, 39);
+      const AIMA_GLOBAL uint8_t* base = q < 16 ? dsc : q < 20 ? dzp : q < 36 ? ssc : szp;
+      const uint32_t off = q < 16   ? (uint32_t)h0 * 8 + 4 * q
+                           : q < 20 ? (uint32_t)h0 * 2 + 4 * (q - 16)
+                           : q < 36 ? (uint32_t)h0 * 8 + 4 * (q - 20)
+                                    : (uint32_t)h0 * 2 + 4 * (q - 36);
+      gsb_n = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
+    }
   };
   // this wave's 256 norm-weight floats and gate-vector halves: lane l holds
   // values 256 w + 4 l .. +3
@@ -676,10 +1010,76 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     nw_n = gload16(Ly.norm + v0);
     gv_n = *reinterpret_cast<const AIMA_GLOBAL u32x2*>(uptr(Ly.gate_vec) + v0 * 2);
   };
+  // routed plan: this wave's router row, expert 8j + w (clamped onto the
+  // last expert past the expert count), one 32-value chunk per lane
+  u32x4 rw = {}, rw_n = {};
+  uint32_t rsw = 0, rsw_n = 0, rzw = 0, rzw_n = 0;
+  auto router_row = [&]() { return min(j * kWaves + wave, a.experts - 1); };
+  auto prefetch_router = [&](int L) {
+    const int ln = opaque_v(threadIdx.x & 63);
+    const PlanLayer& Ly = S.table[L];
+    const int e = router_row();
+    const int gi = e * gA + ((ln * 32) >> glog2);
+    rw_n = ld_w(uptr(Ly.rq), (uint32_t)e * (kH / 2) + ln * 16);
+    rsw_n = ld_u32(uptr(Ly.rs), (gi * 2) & ~3);
+    rzw_n = ld_u32(uptr(Ly.rz), (gi >> 1) & ~3);
+  };
+  // Moves the prefetched rows into the working registers (with 128-wide
+  // groups, hands the gathered scale and zero-point words to their lanes).
+  auto rotate_a = [&]() {
+    const int ln = opaque_v(threadIdx.x & 63);
+#pragma unroll
+    for (int i = 0; i < kMaxRowsA; ++i) wa[i] = wa_n[i];
+    if (g128) {
+      // lane l: gate/up group l / 4 of row slot i
+#pragma unroll
+      for (int i = 0; i < kMaxRowsA; ++i) {
+        sa[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((8 * i + (ln >> 3)) * 4, (int)gsa_n);
+        za[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((40 + 2 * i + (ln >> 5)) * 4, (int)gsa_n);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < kMaxRowsA; ++i) {
+        sa[i] = sa_n[i];
+        za[i] = za_n[i];
+      }
+    }
+  };
+  auto rotate_b = [&]() {
+    const int ln = opaque_v(threadIdx.x & 63);
+#pragma unroll
+    for (int u = 0; u < 3; ++u) wb[u] = wb_n[u];
+    if (g128) {
+      // down routed row 4u + l / 16, group (l & 15) / 4; shared row
+      // (l & 15) / 2, group x / 2
+      auto pick = [](uint32_t v, int src) {
+        return (uint32_t)__builtin_amdgcn_ds_bpermute(src * 4, (int)v);
+      };
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = 4 * u + (ln >> 4);
+        sb[u] = pick(gsb_n, 2 * r + ((ln & 15) >> 3));
+        zb[u] = pick(gsb_n, 16 + (r >> 1));
+      }
+      const int r8 = (ln & 15) >> 1;
+      sb[2] = pick(gsb_n, 20 + 2 * r8 + (x >> 2));
+      zb[2] = pick(gsb_n, 36 + (r8 >> 1));
+    } else {
+#pragma unroll
+      for (int u = 0; u < 3; ++u) {
+        sb[u] = sb_n[u];
+        zb[u] = zb_n[u];
+      }
+    }
+  };
 
   load_vec(0);
-  prefetch_a(0);
-  prefetch_b(0);
+  if (ROUTED) {
+    prefetch_router(0);
+  } else {
+    prefetch_a(S.table[0], slot_expert(0));
+    prefetch_b(S.table[0], slot_expert(0));
+  }
   AIMA_TRACE(40, 1, 0);  // prologue done
 
   for (int L = 0; L < a.n_layers; ++L) {
@@ -734,41 +1134,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       finish();
       return;
     }
-#pragma unroll
-    for (int i = 0; i < kMaxRowsA; ++i) wa[i] = wa_n[i];
-#pragma unroll
-    for (int u = 0; u < 3; ++u) wb[u] = wb_n[u];
-    if (g128) {
-      // lane l: gate/up group l / 4 of row slot i; down routed row
-      // 4u + l / 16, group (l & 15) / 4; shared row (l & 15) / 2, group x / 2
-      auto pick = [](uint32_t v, int src) {
-        return (uint32_t)__builtin_amdgcn_ds_bpermute(src * 4, (int)v);
-      };
-#pragma unroll
-      for (int i = 0; i < kMaxRowsA; ++i) {
-        sa[i] = pick(gsa_n, 8 * i + (ln >> 3));
-        za[i] = pick(gsa_n, 40 + 2 * i + (ln >> 5));
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int r = 4 * u + (ln >> 4);
-        sb[u] = pick(gsb_n, 2 * r + ((ln & 15) >> 3));
-        zb[u] = pick(gsb_n, 16 + (r >> 1));
-      }
-      const int r8 = (ln & 15) >> 1;
-      sb[2] = pick(gsb_n, 20 + 2 * r8 + (x >> 2));
-      zb[2] = pick(gsb_n, 36 + (r8 >> 1));
+    if (!ROUTED) {
+      rotate_a();
+      rotate_b();
     } else {
-#pragma unroll
-      for (int i = 0; i < kMaxRowsA; ++i) {
-        sa[i] = sa_n[i];
-        za[i] = za_n[i];
-      }
-#pragma unroll
-      for (int u = 0; u < 3; ++u) {
-        sb[u] = sb_n[u];
-        zb[u] = zb_n[u];
-      }
+      rw = rw_n;
+      rsw = rsw_n;
+      rzw = rzw_n;
     }
     nw = nw_n;
     gv = gv_n;
@@ -816,26 +1188,112 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     }
     __syncthreads();  // #2: A operands ready
     AIMA_TRACE(L, 2, 0);
-    if (L + 1 < a.n_layers) {
+    if (!ROUTED && L + 1 < a.n_layers) {
       load_vec(L + 1);
-      prefetch_b(L + 1);
+      prefetch_b(S.table[L + 1], slot_expert(L + 1));
     }
     {
       XChunk xc;
       get_chunk(S.xa_p, S.xa_bias, S.xa_xsum, ln, xc);
+      if (ROUTED) {
+        // router logit of expert 8j + w, published to the XCD
+        const int e = j * kWaves + wave;
+        const int gi = router_row() * gA + ((ln * 32) >> glog2);
+        const float lg =
+            segment_sum<64>(u4_chunk_dot(rw, xc, nib(rzw, gi), scl(rsw, gi), magic));
+        if (lane == 0 && e < a.experts) {
+          st_local64(&a.lgx[((size_t)x * 2 + par) * kRouterRows + e], pack_f32(lg, epA));
+          if (x == 0 && a.logits_out) a.logits_out[(size_t)L * a.experts + e] = lg;
+        }
+        // waves 0 and 1: all logits of the layer (lane l: experts
+        // l + 64 t); wave 0 ranks them, wave 1 computes the probabilities
+        // (the same in every block)
+        float pv[4];
+        if (wave < 2) {
+          const uint64_t* src = a.lgx + ((size_t)x * 2 + par) * kRouterRows + ln;
+          uint64_t v[4];
+          uint32_t spins = 0;
+          while (true) {
+            poll4(src, 64 * 8, v);
+            bool ok = true;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              ok = ok && (ln + 64 * t >= a.experts || (uint32_t)(v[t] >> 32) == epA);
+            if (__all(ok)) break;
+            if (++spins > kSpinLimit) {
+              fail_timeout();
+              break;
+            }
+          }
+          AIMA_TRACE(L, 11, 0);  // logits read
+          float lv[4];
+#pragma unroll
+          for (int t = 0; t < 4; ++t) lv[t] = as_f32((uint32_t)v[t]);
+          if (wave == 0) {
+            const int rank_id = rank_logits(lv, a.experts, k);
+            if (ln <= k) S.rank[ln] = rank_id;
+            if (ln < k) S.route_id[L][ln] = rank_id;
+          } else {
+            softmax_probs(lv, a.experts, pv);
+          }
+        }
+        __syncthreads();  // #2b: the layer's route by the ranking
+        AIMA_TRACE(L, 12, 0);
+        if (S.abort) {
+          finish();
+          return;
+        }
+        // the layer's gate/up and down rows from that route (wave 1 first
+        // checks it: an issue into a full memory queue would hold the check
+        // behind the loads)
+        if (wave != 1) {
+          issue_rows(L);
+          AIMA_TRACE(L, 14, 128);  // loads issued (wave 2)
+        } else {
+          int id = ln <= k ? S.rank[ln] : -1;
+          float w = 0.f;
+          const bool same = route_confirm(pv, a.experts, id, k, a.min_weight_sum, w);
+          if (!same) select_probs(pv, a.experts, k, a.min_weight_sum, id, w);
+          if (ln < k) {
+            // non-finite logits select nothing: flagged, the slot is dropped
+            if (id < 0 || id >= a.experts) {
+              atomicOr(a.err, AIMA_DEVERR_EXPERT_RANGE);
+              id = -1;
+            }
+            S.route_id[L][ln] = id;
+            S.route_w[L][ln] = w;
+            if (b == 0 && a.ids_out) a.ids_out[L * k + ln] = id;
+            if (b == 0 && a.w_out) a.w_out[L * k + ln] = w;
+          }
+          if (ln == 0) S.reroute = same ? 0 : 1;
+          AIMA_TRACE(L, 15, 64);  // route confirmed (wave 1)
+          wave_lds_sync();
+          issue_rows(L);
+        }
+        __syncthreads();  // #2c: the layer's final route
+        AIMA_TRACE(L, 13, 0);
+        if (S.reroute) issue_rows(L);
+        rotate_a();
+      }
 #pragma unroll
       for (int i = 0; i < kMaxRowsA; ++i) {
         const int ri = ((wave + 4) & 7) + kWaves * i;
-        // one row of the next layer per dot product (kept in place)
-        if (L + 1 < a.n_layers) prefetch_a1(L + 1, i);
-        __builtin_amdgcn_sched_barrier(0);
-        if (ri < kRowsA) {
-          const int p = j * kPairs + (ri >> 1);
+        if (!ROUTED) {
+          // one row of the next layer per dot product (kept in place)
+          if (L + 1 < a.n_layers) prefetch_a1(S.table[L + 1], slot_expert(L + 1), i);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        // The routed plan has no prefetch to pace: every slot is computed
+        // (a surplus one on the clamped row it loaded, result dropped) so the
+        // dot products of the five rows can interleave.
+        if (ROUTED || ri < kRowsA) {
+          const int rc = min(ri, kRowsA - 1);
+          const int p = j * kPairs + (rc >> 1);
           const int unit = p < kI ? p : x * kSlice + (p - kI);
           const int gi = unit * gA + ((ln * 32) >> glog2);
           const float dd =
               segment_sum<64>(u4_chunk_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
-          if (lane == 0) S.rowsum[ri] = dd;
+          if (lane == 0 && ri < kRowsA) S.rowsum[ri] = dd;
         }
       }
     }
@@ -909,6 +1367,15 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     if (S.abort) {
       finish();
       return;
+    }
+    if (ROUTED) {
+      // the next layer's vectors and router rows (needed from its RMSNorm
+      // on), then this layer's down rows into the working registers
+      if (L + 1 < a.n_layers) {
+        load_vec(L + 1);
+        prefetch_router(L + 1);
+      }
+      rotate_b();
     }
     // ================= phase B_L =================
     {
@@ -1033,8 +1500,11 @@ struct aima_moe_decode_plan {
   uint64_t* pbuf = nullptr;
   uint32_t* route_ids = nullptr;
   uint64_t* route_w = nullptr;
+  uint64_t* lgx = nullptr;
   uint32_t* counter = nullptr;
   uint32_t* err = nullptr;
+  std::vector<PlanLayer> host;  // the uploaded table
+  bool routers = false;         // router rows present in the table
 };
 
 namespace {
@@ -1094,12 +1564,12 @@ PlanLayer plan_layer(const aima_moe_layer& L) {
   PlanLayer p{};
   for (int h = 0; h < 2; ++h) {
     const int64_t r0 = r.row(0, h, 0), s0 = s.row(0, h, 0);
-    p.gq[h] = r.q[h] + r0 * (L.hidden / 2);
-    p.gs[h] = r.s[h] + r0 * G;
-    p.gz[h] = r.z[h] + r0 * G / 2;
-    p.sq[h] = s.q[h] + s0 * (L.hidden / 2);
-    p.ss[h] = s.s[h] + s0 * G;
-    p.sz[h] = s.z[h] + s0 * G / 2;
+    (h ? p.gq1 : p.gq0) = r.q[h] + r0 * (L.hidden / 2);
+    (h ? p.gs1 : p.gs0) = r.s[h] + r0 * G;
+    (h ? p.gz1 : p.gz0) = r.z[h] + r0 * G / 2;
+    (h ? p.sq1 : p.sq0) = s.q[h] + s0 * (L.hidden / 2);
+    (h ? p.ss1 : p.ss0) = s.s[h] + s0 * G;
+    (h ? p.sz1 : p.sz0) = s.z[h] + s0 * G / 2;
   }
   p.estride_q = (uint32_t)(r.expert_rows * (L.hidden / 2));
   p.estride_s = (uint32_t)(r.expert_rows * G * 2);
@@ -1130,12 +1600,15 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   int cus = 0, coop = 0, per_cu = 0;
   AIMA_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   AIMA_HIP(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev));
-  int per_cu128 = 0;
-  AIMA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_persistent_kernel<false>,
-                                                        kThreads, 0));
-  AIMA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-      &per_cu128, decode_persistent_kernel<true>, kThreads, 0));
-  per_cu = std::min(per_cu, per_cu128);
+  per_cu = 1 << 30;
+  for (const void* kern : {reinterpret_cast<const void*>(decode_persistent_kernel<false, false>),
+                           reinterpret_cast<const void*>(decode_persistent_kernel<true, false>),
+                           reinterpret_cast<const void*>(decode_persistent_kernel<false, true>),
+                           reinterpret_cast<const void*>(decode_persistent_kernel<true, true>)}) {
+    int n = 0;
+    AIMA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, 0));
+    per_cu = std::min(per_cu, n);
+  }
   const int blocks = kBlocks;  // one block per CU: 8 XCDs x 32 CUs
   (void)coop;
   if (cus != kBlocks || per_cu < 1) {
@@ -1156,6 +1629,7 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   const size_t o_p = take(sizeof(uint64_t) * 2 * kH * kXcds);
   const size_t o_rid = take(sizeof(uint32_t) * n_layers * k);
   const size_t o_rw = take(sizeof(uint64_t) * n_layers * k);
+  const size_t o_lgx = take(sizeof(uint64_t) * kXcds * 2 * kRouterRows);
   const size_t o_ctr = take(256);
   aima_moe_decode_plan* p = new aima_moe_decode_plan();
   p->device = dev;
@@ -1176,12 +1650,14 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   p->pbuf = reinterpret_cast<uint64_t*>(p->mem + o_p);
   p->route_ids = reinterpret_cast<uint32_t*>(p->mem + o_rid);
   p->route_w = reinterpret_cast<uint64_t*>(p->mem + o_rw);
+  p->lgx = reinterpret_cast<uint64_t*>(p->mem + o_lgx);
   p->counter = reinterpret_cast<uint32_t*>(p->mem + o_ctr);
   e = hipMemset(p->mem, 0, off);
   if (e == hipSuccess) {
-    std::vector<PlanLayer> host(n_layers);
-    for (int l = 0; l < n_layers; ++l) host[l] = plan_layer(layers[l]);
-    e = hipMemcpy(p->table, host.data(), sizeof(PlanLayer) * n_layers, hipMemcpyHostToDevice);
+    p->host.resize(n_layers);
+    for (int l = 0; l < n_layers; ++l) p->host[l] = plan_layer(layers[l]);
+    e = hipMemcpy(p->table, p->host.data(), sizeof(PlanLayer) * n_layers,
+                  hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) {
     (void)hipFree(p->mem);
@@ -1191,6 +1667,43 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   *plan = p;
   return AIMA_OK;
 }
+
+namespace {
+
+int plan_launch(aima_moe_decode_plan* plan, PersistArgs& a, bool routed, void* stream) {
+  int dev = 0;
+  AIMA_HIP(hipGetDevice(&dev));
+  AIMA_REQUIRE(dev == plan->device, "moe_decode_plan_run: plan belongs to another device");
+  a.layers = plan->table;
+  a.n_layers = plan->n_layers;
+  a.k = plan->k;
+  a.experts = plan->experts;
+  a.group_log2 = plan->group_log2;
+  a.rx = plan->rx;
+  a.actx = plan->actx;
+  a.pbuf = plan->pbuf;
+  a.route_ids = plan->route_ids;
+  a.route_w = plan->route_w;
+  a.lgx = plan->lgx;
+  a.epoch_counter = plan->counter;
+  a.err = plan->err;
+  void* args[] = {&a};
+  const bool g128 = plan->group_log2 == 7;
+  const void* kern =
+      routed ? (g128 ? reinterpret_cast<const void*>(decode_persistent_kernel<true, true>)
+                     : reinterpret_cast<const void*>(decode_persistent_kernel<false, true>))
+             : (g128 ? reinterpret_cast<const void*>(decode_persistent_kernel<true, false>)
+                     : reinterpret_cast<const void*>(decode_persistent_kernel<false, false>));
+  // A regular launch: with one block per CU on 256 CUs every block becomes
+  // resident (work of other streams only delays placement).  A cooperative
+  // launch would guarantee it against concurrent persistent launches too,
+  // but measured 18 us slower per launch (the gap between launches).
+  AIMA_HIP(hipLaunchKernel(kern, dim3(plan->blocks), dim3(kThreads), args, 0,
+                           (hipStream_t)stream));
+  return AIMA_OK;
+}
+
+}  // namespace
 
 extern "C" int aima_moe_decode_plan_run(aima_moe_decode_plan* plan, float eps,
                                         const uint16_t* residual_in,
@@ -1202,16 +1715,7 @@ extern "C" int aima_moe_decode_plan_run(aima_moe_decode_plan* plan, float eps,
                "moe_decode_plan_run: need router logits or ids + weights");
   AIMA_REQUIRE(min_weight_sum > 0.f, "moe_decode_plan_run: minimum weight sum must be positive");
   AIMA_REQUIRE(aligned(residual_in, 16), "moe_decode_plan_run: residual_in must be 16-byte aligned");
-  int dev = 0;
-  AIMA_HIP(hipGetDevice(&dev));
-  AIMA_REQUIRE(dev == plan->device, "moe_decode_plan_run: plan belongs to another device");
-  hipStream_t st = (hipStream_t)stream;
   PersistArgs a{};
-  a.layers = plan->table;
-  a.n_layers = plan->n_layers;
-  a.k = plan->k;
-  a.experts = plan->experts;
-  a.group_log2 = plan->group_log2;
   a.logits = router_logits;
   a.ids_in = ids;
   a.w_in = weights;
@@ -1219,23 +1723,63 @@ extern "C" int aima_moe_decode_plan_run(aima_moe_decode_plan* plan, float eps,
   a.eps = eps;
   a.r0 = residual_in;
   a.out = out;
-  a.rx = plan->rx;
-  a.actx = plan->actx;
-  a.pbuf = plan->pbuf;
-  a.route_ids = plan->route_ids;
-  a.route_w = plan->route_w;
-  a.epoch_counter = plan->counter;
-  a.err = plan->err;
-  void* args[] = {&a};
-  const void* kern = plan->group_log2 == 7
-                         ? reinterpret_cast<const void*>(decode_persistent_kernel<true>)
-                         : reinterpret_cast<const void*>(decode_persistent_kernel<false>);
-  // A regular launch: with one block per CU on 256 CUs every block becomes
-  // resident (work of other streams only delays placement).  A cooperative
-  // launch would guarantee it against concurrent persistent launches too,
-  // but measured 18 us slower per launch (the gap between launches).
-  AIMA_HIP(hipLaunchKernel(kern, dim3(plan->blocks), dim3(kThreads), args, 0, st));
+  return plan_launch(plan, a, false, stream);
+}
+
+extern "C" int aima_moe_decode_plan_set_routers(aima_moe_decode_plan* plan,
+                                                const aima_u4_tensor* routers) {
+  AIMA_REQUIRE(plan && routers, "moe_decode_plan_set_routers: null pointer");
+  if (plan->experts > kRouterRows) {
+    return fail(AIMA_E_UNSUPPORTED,
+                "moe_decode_plan_set_routers: the routed plan takes at most 256 experts");
+  }
+  for (int l = 0; l < plan->n_layers; ++l) {
+    const aima_u4_tensor& R = routers[l];
+    AIMA_REQUIRE(R.qweight && R.scale && R.zp, "moe_decode_plan_set_routers: null router tensor");
+    AIMA_REQUIRE(aligned(R.qweight, 16) && aligned(R.scale, 4) && aligned(R.zp, 4),
+                 "moe_decode_plan_set_routers: router qweight must be 16-byte aligned, "
+                 "scale and zp 4-byte aligned");
+  }
+  int dev = 0;
+  AIMA_HIP(hipGetDevice(&dev));
+  AIMA_REQUIRE(dev == plan->device, "moe_decode_plan_set_routers: plan belongs to another device");
+  std::vector<PlanLayer> host = plan->host;
+  for (int l = 0; l < plan->n_layers; ++l) {
+    host[l].rq = routers[l].qweight;
+    host[l].rs = routers[l].scale;
+    host[l].rz = routers[l].zp;
+  }
+  // setup time: no run of this plan may be in flight while the table changes
+  AIMA_HIP(hipDeviceSynchronize());
+  AIMA_HIP(hipMemcpy(plan->table, host.data(), sizeof(PlanLayer) * plan->n_layers,
+                     hipMemcpyHostToDevice));
+  plan->host.swap(host);
+  plan->routers = true;
   return AIMA_OK;
+}
+
+extern "C" int aima_moe_decode_plan_run_routed(aima_moe_decode_plan* plan, float eps,
+                                               const uint16_t* residual_in, float min_weight_sum,
+                                               int32_t* ids, float* weights, float* logits,
+                                               uint16_t* out, void* stream) {
+  AIMA_REQUIRE(plan && residual_in && out, "moe_decode_plan_run_routed: null pointer");
+  if (!plan->routers) {
+    return fail(AIMA_E_INVALID,
+                "moe_decode_plan_run_routed: no routers (aima_moe_decode_plan_set_routers)");
+  }
+  AIMA_REQUIRE(min_weight_sum > 0.f,
+               "moe_decode_plan_run_routed: minimum weight sum must be positive");
+  AIMA_REQUIRE(aligned(residual_in, 16),
+               "moe_decode_plan_run_routed: residual_in must be 16-byte aligned");
+  PersistArgs a{};
+  a.min_weight_sum = min_weight_sum;
+  a.eps = eps;
+  a.r0 = residual_in;
+  a.out = out;
+  a.logits_out = logits;
+  a.ids_out = ids;
+  a.w_out = weights;
+  return plan_launch(plan, a, true, stream);
 }
 
 extern "C" int aima_moe_decode_plan_error(aima_moe_decode_plan* plan, uint32_t* error_bits,

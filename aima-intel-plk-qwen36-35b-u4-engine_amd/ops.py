@@ -390,6 +390,14 @@ class RouterTopKSelection:
 
 
 @dataclass
+class DecodeRoutes:
+    """What a routed DecodePlan run chose for every layer of the token."""
+    expert_ids: torch.Tensor  # int32 [L, k], rank order
+    weights: torch.Tensor     # float32 [L, k] normalized router weights
+    logits: torch.Tensor      # float32 [L, E] router logits
+
+
+@dataclass
 class Qwen36MoeFfnLayerResult:
     """``Qwen36MoeFfnLayerResult`` (gguf_loader.hpp:144-161), as device
     tensors: every intermediate of one decode FFN layer (ffn_layer_trace)."""
@@ -735,7 +743,12 @@ class DecodePlan:
     uploads the layer table once; ``run`` executes RMSNorm -> MoE FFN ->
     residual for every layer in a single persistent kernel (graph-capturable,
     no allocation).  Routing comes from ``router_logits`` [L, E] (the
-    select_router_topk rule) or from ``ids``/``weights`` [L, k].
+    select_router_topk rule) or from ``ids``/``weights`` [L, k].  With
+    ``routers`` (one U4 router [experts][hidden] per layer, experts <= 256)
+    ``run(residual, routers=...)`` is true decode: every layer routes from its
+    own normalized input inside the same launch, as run_qwen36_moe_ffn_layer
+    does (gguf_loader.cpp:5704-5711); the chosen ids, weights and logits can
+    be captured through ``route_out``.
     Raises AimaError(AIMA_E_UNSUPPORTED) for shapes outside the specialization
     (hidden 2048, inter 512, k <= 8); ``moe_stack_decode`` covers those.
     ``run`` is asynchronous: its output is valid only if ``check()`` (or
@@ -743,7 +756,8 @@ class DecodePlan:
     its spin limit leaves ``out`` unwritten.
     """
 
-    def __init__(self, layers: Sequence[MoeLayerWeights], k: int = 8):
+    def __init__(self, layers: Sequence[MoeLayerWeights], k: int = 8,
+                 routers: Optional[Sequence[U4Weight]] = None):
         self.layers = list(layers)  # keep the weights alive
         self.k = int(k)
         self.hidden = self.layers[0].hidden
@@ -751,11 +765,38 @@ class DecodePlan:
         h = C.c_void_p(0)
         call("aima_moe_decode_plan_create", self._arr, len(self.layers), self.k, C.byref(h))
         self._h = h
+        self.routers = None
+        if routers is not None:
+            self.set_routers(routers)
+
+    def set_routers(self, routers: Sequence[U4Weight]) -> None:
+        """Registers one router per layer for true decode (setup time: waits
+        for the device, then uploads the router rows into the plan)."""
+        if self._h is None:
+            raise RuntimeError("decode plan was closed")
+        routers = list(routers)
+        L = len(self.layers)
+        if len(routers) != L:
+            raise ValueError("one router per layer")
+        _require_cuda(*[r.qweight for r in routers])
+        for lay, r in zip(self.layers, routers):
+            if r.experts * r.rows != lay.experts or r.k != lay.hidden or r.group != lay.group:
+                raise ValueError("router must be [experts][hidden] at the layer's group")
+        rt = (_lib.U4TensorC * L)(*[_lib.U4TensorC(r.qweight.data_ptr(), r.scale.data_ptr(),
+                                                    r.zp.data_ptr()) for r in routers])
+        call("aima_moe_decode_plan_set_routers", self._h, rt)
+        self.routers = routers  # keep the router weights alive
 
     def run(self, residual: torch.Tensor, router_logits: Optional[torch.Tensor] = None,
             ids: Optional[torch.Tensor] = None, weights: Optional[torch.Tensor] = None,
             epsilon: float = 1e-6, min_weight_sum: float = MIN_WEIGHT_SUM,
-            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+            out: Optional[torch.Tensor] = None,
+            routers: Optional[Sequence[U4Weight]] = None,
+            route_out: Optional[DecodeRoutes] = None) -> torch.Tensor:
+        """One token through every layer.  ``routers``: route each layer on
+        the device from its own normalized input (registered on first use;
+        pass the same list again for the fast path).  ``route_out``: a
+        DecodeRoutes (``plan.route_buffers()``) that the routed run fills."""
         if self._h is None:
             raise RuntimeError("decode plan was closed")
         _require_cuda(residual, router_logits, ids, weights, out)
@@ -763,6 +804,15 @@ class DecodePlan:
         if residual.dtype != torch.float16 or residual.numel() != self.hidden or \
                 not residual.is_contiguous() or residual.data_ptr() % 16:
             raise ValueError("residual must be a contiguous, 16-byte aligned float16 [hidden]")
+        if routers is not None or route_out is not None:
+            if router_logits is not None or ids is not None or weights is not None:
+                raise ValueError("routers and router_logits / ids are exclusive")
+            if routers is not None and (self.routers is None or len(routers) != L or any(
+                    a is not b for a, b in zip(routers, self.routers))):
+                self.set_routers(routers)
+            if self.routers is None:
+                raise ValueError("no routers registered")
+            return self._run_routed(residual, epsilon, min_weight_sum, out, route_out)
         if router_logits is not None:
             if router_logits.dtype != torch.float32 or router_logits.dim() != 2 or \
                     router_logits.shape[0] != L or not router_logits.is_contiguous():
@@ -781,6 +831,39 @@ class DecodePlan:
         call("aima_moe_decode_plan_run", self._h, float(epsilon), residual.data_ptr(),
              _ptr(router_logits), _ptr(ids), _ptr(weights), float(min_weight_sum),
              out.data_ptr(), _stream())
+        return out
+
+    def route_buffers(self, device=None) -> DecodeRoutes:
+        """Empty [L, k] ids / weights and [L, E] logits for ``route_out``."""
+        L, E = len(self.layers), self.layers[0].experts
+        dev = device if device is not None else self.layers[0].norm_weight.device
+        return DecodeRoutes(
+            expert_ids=torch.empty((L, self.k), dtype=torch.int32, device=dev),
+            weights=torch.empty((L, self.k), dtype=torch.float32, device=dev),
+            logits=torch.empty((L, E), dtype=torch.float32, device=dev))
+
+    def _run_routed(self, residual, epsilon, min_weight_sum, out, route_out):
+        L, E = len(self.layers), self.layers[0].experts
+        if out is None:
+            out = torch.empty(self.hidden, dtype=torch.float16, device=residual.device)
+        elif out.dtype != torch.float16 or out.numel() != self.hidden or not out.is_contiguous():
+            raise ValueError("out must be a contiguous float16 [hidden]")
+        ids_p = w_p = lg_p = None
+        if route_out is not None:
+            ids, w, lg = route_out.expert_ids, route_out.weights, route_out.logits
+            _require_cuda(ids, w, lg)
+            if ids.dtype != torch.int32 or tuple(ids.shape) != (L, self.k) or \
+                    not ids.is_contiguous():
+                raise ValueError("route_out.expert_ids must be contiguous int32 [layers, k]")
+            if w.dtype != torch.float32 or tuple(w.shape) != (L, self.k) or \
+                    not w.is_contiguous():
+                raise ValueError("route_out.weights must be contiguous float32 [layers, k]")
+            if lg.dtype != torch.float32 or tuple(lg.shape) != (L, E) or \
+                    not lg.is_contiguous():
+                raise ValueError("route_out.logits must be contiguous float32 [layers, experts]")
+            ids_p, w_p, lg_p = ids.data_ptr(), w.data_ptr(), lg.data_ptr()
+        call("aima_moe_decode_plan_run_routed", self._h, float(epsilon), residual.data_ptr(),
+             float(min_weight_sum), ids_p, w_p, lg_p, out.data_ptr(), _stream())
         return out
 
     def error_bits(self) -> int:

@@ -345,7 +345,15 @@ def main():
                       max(10, args.steps // 10), warmup=3)
     log(f"decode multi-kernel, routed from h: {routed_us:.1f} us/token")
     ws.check()
-    del routers
+    # true decode inside the resident plan: every layer routes from its own
+    # normalized input in the same persistent launch
+    rplan = ops.DecodePlan(layers, k=K_TOP, routers=routers)
+    routed_plan_us = timed(torch, lambda: rplan.run(x, routers=routers, epsilon=EPS, out=out),
+                           args.steps, warmup=args.warmup)
+    rplan.check()
+    log(f"decode persistent, routed from h: {routed_plan_us:.1f} us/token")
+    rplan.close()
+    del rplan, routers
     plan = ops.DecodePlan(layers, k=K_TOP)
 
     def decode_step():
@@ -393,6 +401,7 @@ def main():
                    "graph_us": round(graph_us, 2), "mode": decode_mode,
                    "multikernel_us": round(multi_us, 2),
                    "routed_multikernel_us": round(routed_us, 2),
+                   "routed_plan_us": round(routed_plan_us, 2),
                    "algorithmic_bytes": weight_bytes + act_bytes,
                    "hbm_gbs": round(decode_gbs, 1),
                    "hbm_frac": round(decode_gbs / HBM_PEAK_GBS, 4),

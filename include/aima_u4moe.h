@@ -517,6 +517,26 @@ int aima_moe_decode_plan_run(aima_moe_decode_plan* plan, float eps,
                              const float* router_logits, const int32_t* ids,
                              const float* weights, float min_weight_sum,
                              uint16_t* out, void* stream);
+/* True decode in the resident plan.  set_routers registers one U4 router
+ * per layer (routers[n_layers], each [experts][hidden] at the layer's
+ * group; experts <= 256; qweight 16-byte, scale and zp 4-byte aligned;
+ * setup time: waits for the device, then uploads).  run_routed then routes
+ * every layer from its own normalized input inside the same launch, as
+ * run_qwen36_moe_ffn_layer does per layer (engine/src/gguf_loader.cpp:
+ * 5704-5711): h = f16(rmsnorm(r_L)), logits = U4 FC(router_L, h) in f32,
+ * then the select_router_topk rule (gguf_loader.hpp:371-373), then the
+ * layer's experts.  Optional outputs (NULL to skip): ids / weights
+ * [n_layers][k] (rank order, normalized weights) and logits
+ * [n_layers][experts].  Asynchronous, allocates nothing, graph-capturable,
+ * with the same concurrency rules as aima_moe_decode_plan_run.  Non-finite
+ * logits select no expert: AIMA_DEVERR_EXPERT_RANGE is set and the slot
+ * contributes nothing.  AIMA_E_INVALID before set_routers. */
+int aima_moe_decode_plan_set_routers(aima_moe_decode_plan* plan,
+                                     const aima_u4_tensor* routers);
+int aima_moe_decode_plan_run_routed(aima_moe_decode_plan* plan, float eps,
+                                    const uint16_t* residual_in, float min_weight_sum,
+                                    int32_t* ids, float* weights, float* logits,
+                                    uint16_t* out, void* stream);
 /* Device error bits of the plan (AIMA_DEVERR_*; synchronizes, then clears). */
 int aima_moe_decode_plan_error(aima_moe_decode_plan* plan, uint32_t* error_bits,
                                void* stream);
