@@ -468,6 +468,15 @@ __device__ __forceinline__ void router_select_wave(const float* __restrict__ l, 
   out_p = my_p;
 }
 
+// Orders one wave's LDS writes before its following LDS reads by other lanes
+// of the same wave (a wave executes its LDS operations in order; the fences
+// keep the compiler from moving the accesses across).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) {
   const float s = g >= 0.f ? 1.f / (1.f + expf(-g)) : expf(g) / (1.f + expf(g));
   return g * s * u;

@@ -6,12 +6,11 @@
 // NaN values are never chosen; with fewer than k numbers the remaining
 // ranks hold the empty pair (-inf, 0x7fffffff).
 //
-// One launch.  P <= 256 blocks of 1024 threads; block b owns a contiguous
-// chunk of at most 4096 values (4 per thread) and selects its k best
-// (block_select) into its partial slots.  The block that arrives last at a
-// device-scope counter in the workspace header selects the final k from
-// the P * k partials (see topk_kernel for how it knows they are all
-// written) and clears the counter.  P = 1 writes the result directly.
+// One launch.  P <= 256 blocks of 256 threads (one wave per SIMD); block b
+// owns a contiguous chunk of at most 4096 values (16 per thread) and selects
+// its k best (block_select) into its partial slots.  Block 0 then selects
+// the final k from the P * k partials once every slot carries the launch's
+// epoch (see topk_kernel).  P = 1 writes the result directly.
 // n <= 1,048,576.
 //
 // The LM head (aima_u4_lm_head_topk) is the U4 matvec into the caller's
@@ -36,22 +35,27 @@ namespace {
 
 constexpr int kTopkMax = 16;
 constexpr int kNoIndex = 0x7fffffff;
-constexpr int kPassThreads = 1024;
-constexpr int kPerThread = 4;
+constexpr int kPassThreads = 256;
+constexpr int kPerThread = 16;  // the final selection: P * k <= 256 * 16 picks
 constexpr int kMaxPartials = 256;
 constexpr int64_t kChunkMax = (int64_t)kPassThreads * kPerThread;
 constexpr int64_t kTopkMaxN = kChunkMax * kMaxPartials;
+
 constexpr int kWaves = kPassThreads / 64;
+constexpr int kRowBests = kWaves * 4;  // one best per 16-lane row
+static_assert(kRowBests >= kTopkMax, "the threshold needs k row bests");
 constexpr int kMaxCand = 256;  // candidates one wave selects from (4 per lane)
 
-// The selection's block counter and epoch, kept in the workspace header at
-// byte 128 (the error word is at 0): the counter is zero in a fresh
-// (zero-filled) workspace and the last block of every launch leaves it zero
-// again; the epoch (any start value) advances by one per launch.
-constexpr size_t kTopkCounterOffset = 128;
+// The selection's launch counter, kept in the workspace header at byte 132
+// (the error word is at 0; bytes 128..131 stay zero): any start value, so a
+// zero-filled workspace works, and it advances by one per launch.  A launch
+// tags its picks with 1 + counter % 2047, never 0, so a zero-filled slot is
+// never taken for one written by this launch.
+constexpr size_t kTopkLaunchOffset = 132;
 
+// (bitwise on the comparisons: no short-circuit branches)
 __device__ __forceinline__ bool better(float av, int ai, float bv, int bi) {
-  return av > bv || (av == bv && ai < bi);
+  return (av > bv) | ((av == bv) & (ai < bi));
 }
 
 // k rounds of a wave-wide maximum over PER candidates per lane; lane r ends
@@ -92,62 +96,90 @@ __device__ __forceinline__ void wave_topk(float (&v)[PER], int (&ix)[PER], int k
 struct SelectLds {
   float v[kWaves * kTopkMax];
   int i[kWaves * kTopkMax];
-  float wv[kWaves];
-  int wi[kWaves];
-  int cnt[kWaves];
-  float cv[kMaxCand];
-  int ci[kMaxCand];
-  int is_last;
+  alignas(16) float rv[kRowBests];
+  alignas(16) int ri[kRowBests];
+  int count;
+  alignas(16) float cv[kMaxCand];
+  alignas(16) int ci[kMaxCand];
 };
 
 // The block's top-k of PER (value, index) pairs per thread; wave 0 lanes
 // r < k write rank r to out_v / out_i.  Every thread of the block calls it.
 //
-// Threshold filter first: each wave finds its best pair; the k-th best of
-// the 16 wave bests, T, bounds the block's top-k from below (the k wave
-// bests at or above T are k pairs at least as good), so only pairs at or
-// above T can be picked.  They are compacted into LDS (ballots give each its
-// slot).  Up to 64 of them (the usual case: the 16 wave bests and a few
-// more): lane l ranks survivor l against all of them and the survivor of
+// Threshold filter first: every 16-lane row finds its best pair (DPP inside
+// the row); the k-th best of the 16 row bests, T, bounds the block's top-k
+// from below (the k row bests at or above T are k pairs at least as good),
+// so only pairs at or above T can be picked.  Those few are appended to LDS
+// through an LDS counter (their order does not matter: they are ranked by
+// (value, index) next).  Up to 64 of them (the usual case: about the 16 row
+// bests): lane l ranks survivor l against all of them and the survivor of
 // rank r < k is pick r.  Up to 256: wave 0 selects by k rounds of a
 // wave-wide maximum.  When ties leave more than 256, every wave selects its
-// own k and wave 0 merges the 16 lists.
+// own k and wave 0 merges the lists.
 template <int PER>
 __device__ void block_select(float (&v)[PER], int (&ix)[PER], int k, SelectLds& S, float* out_v,
                              int32_t* out_i) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  // wave bests
-  float bv = -INFINITY;
-  int bi = kNoIndex;
+  // row bests: the lane's best by a pairwise tree (independent compares at
+  // each level, not one chain of PER), then DPP inside the row
+  static_assert((PER & (PER - 1)) == 0, "PER is a power of two");
+  float tv_[PER];
+  int ti_[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    if (better(v[j], ix[j], bv, bi)) {
-      bv = v[j];
-      bi = ix[j];
+    // NaN is never chosen: it becomes the empty pair (a NaN kept in the
+    // tree would beat nothing and hide the lane's real values); selects,
+    // not a branch, so the arrays stay in place
+    const bool nan = v[j] != v[j];
+    ix[j] = nan ? kNoIndex : ix[j];
+    v[j] = nan ? -INFINITY : v[j];
+    tv_[j] = v[j];
+    ti_[j] = ix[j];
+  }
+#pragma unroll
+  for (int w = PER / 2; w > 0; w /= 2) {
+#pragma unroll
+    for (int j = 0; j < w; ++j) {
+      const bool b = better(tv_[j + w], ti_[j + w], tv_[j], ti_[j]);
+      tv_[j] = b ? tv_[j + w] : tv_[j];
+      ti_[j] = b ? ti_[j + w] : ti_[j];
     }
   }
-  wave_best_pair(bv, bi);
-  if (lane == 0) {
-    S.wv[wave] = bv;
-    S.wi[wave] = bi;
+  const float lane_v = tv_[0];
+  const int lane_i = ti_[0];
+  float bv = lane_v;
+  int bi = lane_i;
+  pair_step<0xB1>(bv, bi);   // quad_perm [1,0,3,2]
+  pair_step<0x4E>(bv, bi);   // quad_perm [2,3,0,1]
+  pair_step<0x141>(bv, bi);  // row_half_mirror
+  pair_step<0x140>(bv, bi);  // row_mirror
+  if ((lane & 15) == 0) {
+    S.rv[wave * 4 + (lane >> 4)] = bv;
+    S.ri[wave * 4 + (lane >> 4)] = bi;
   }
+  if (threadIdx.x == 0) S.count = 0;
   __syncthreads();
-  // T = the k-th best wave best: lane w < 16 ranks wave best w against all 16
+  // T = the k-th best row best: lane r < 16 ranks row best r against all 16
   float tv = -INFINITY;
   int ti = kNoIndex;
   {
-    int rank = kWaves;
+    int rank = kRowBests;
     float mv = -INFINITY;
     int mi = kNoIndex;
-    if (lane < kWaves) {
-      mv = S.wv[lane];
-      mi = S.wi[lane];
+    if (lane < kRowBests) {
+      mv = S.rv[lane];
+      mi = S.ri[lane];
       rank = 0;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) rank += better(S.wv[w], S.wi[w], mv, mi) ? 1 : 0;
+      for (int w = 0; w < kRowBests; w += 4) {
+        const float4 a = *reinterpret_cast<const float4*>(&S.rv[w]);
+        const int4 ia = *reinterpret_cast<const int4*>(&S.ri[w]);
+        rank += (better(a.x, ia.x, mv, mi) ? 1 : 0) + (better(a.y, ia.y, mv, mi) ? 1 : 0) +
+                (better(a.z, ia.z, mv, mi) ? 1 : 0) + (better(a.w, ia.w, mv, mi) ? 1 : 0);
+      }
     }
-    // no rank k-1 (fewer than k waves hold values, their empty bests tie):
+    // no rank k-1 (fewer than k rows hold values, their empty bests tie):
     // no filter, every valid pair qualifies
     const uint64_t hit = __ballot(rank == k - 1);
     if (hit) {
@@ -156,45 +188,51 @@ __device__ void block_select(float (&v)[PER], int (&ix)[PER], int k, SelectLds& 
       ti = __builtin_amdgcn_readlane(mi, src);
     }
   }
-  // compact the pairs at or above T
-  int cnt = 0;
-  bool q[PER];
-  uint64_t mask[PER];
-#pragma unroll
-  for (int j = 0; j < PER; ++j) {
-    q[j] = ix[j] != kNoIndex && (better(v[j], ix[j], tv, ti) || (v[j] == tv && ix[j] == ti));
-    mask[j] = __ballot(q[j]);
-    cnt += __builtin_popcountll(mask[j]);
-  }
-  if (lane == 0) S.cnt[wave] = cnt;
-  __syncthreads();
-  int wbase = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
-    const int c = S.cnt[w];
-    wbase += w < wave ? c : 0;
-    total += c;
-  }
-  if (total <= kMaxCand) {
-    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int off = wbase;
+  // append the pairs at or above T (few: a lane whose own best is below T
+  // holds none, so only the lanes that do scan their values)
+  auto at_or_above = [&](float pv, int pi) {
+    return (pi != kNoIndex) & ((pv > tv) | ((pv == tv) & (pi <= ti)));
+  };
+  if (at_or_above(lane_v, lane_i)) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
-      if (q[j]) {
-        const int slot = off + __builtin_popcountll(mask[j] & below);
-        S.cv[slot] = v[j];
-        S.ci[slot] = ix[j];
+      if (at_or_above(v[j], ix[j])) {
+        const int slot = atomicAdd(&S.count, 1);
+        if (slot < kMaxCand) {
+          S.cv[slot] = v[j];
+          S.ci[slot] = ix[j];
+        }
       }
-      off += __builtin_popcountll(mask[j]);
     }
-    __syncthreads();
+  }
+  __syncthreads();
+  const int total = S.count;
+  if (total <= kMaxCand) {
     if (wave != 0) return;
     if (total <= 64) {
       const bool mine = lane < total;
       const float mv = mine ? S.cv[lane] : -INFINITY;
       const int mi = mine ? S.ci[lane] : kNoIndex;
+      // survivors padded with empty pairs to a multiple of 8, then compared
+      // eight at a time from 16-byte LDS reads (every lane reads the same
+      // words), so the reads are in flight together
+      const int tot8 = (total + 7) & ~7;
+      if (lane >= total && lane < tot8) {
+        S.cv[lane] = -INFINITY;
+        S.ci[lane] = kNoIndex;
+      }
+      wave_lds_sync();
       int rank = 0;
-      for (int j = 0; j < total; ++j) rank += better(S.cv[j], S.ci[j], mv, mi) ? 1 : 0;
+      for (int j = 0; j < tot8; j += 8) {
+        const float4 a = *reinterpret_cast<const float4*>(&S.cv[j]);
+        const float4 b = *reinterpret_cast<const float4*>(&S.cv[j + 4]);
+        const int4 ia = *reinterpret_cast<const int4*>(&S.ci[j]);
+        const int4 ib = *reinterpret_cast<const int4*>(&S.ci[j + 4]);
+        rank += (better(a.x, ia.x, mv, mi) ? 1 : 0) + (better(a.y, ia.y, mv, mi) ? 1 : 0) +
+                (better(a.z, ia.z, mv, mi) ? 1 : 0) + (better(a.w, ia.w, mv, mi) ? 1 : 0) +
+                (better(b.x, ib.x, mv, mi) ? 1 : 0) + (better(b.y, ib.y, mv, mi) ? 1 : 0) +
+                (better(b.z, ib.z, mv, mi) ? 1 : 0) + (better(b.w, ib.w, mv, mi) ? 1 : 0);
+      }
       if (mine && rank < k) {
         out_v[rank] = mv;
         out_i[rank] = mi;
@@ -232,7 +270,7 @@ __device__ void block_select(float (&v)[PER], int (&ix)[PER], int k, SelectLds& 
   }
   __syncthreads();
   if (wave == 0) {
-    constexpr int kCandPer = kWaves * kTopkMax / 64;
+    constexpr int kCandPer = (kWaves * kTopkMax + 63) / 64;
     float c[kCandPer];
     int ci[kCandPer];
 #pragma unroll
@@ -259,16 +297,35 @@ __device__ __forceinline__ uint64_t pack_pick(float v, int ix, uint32_t epoch) {
 }
 constexpr uint32_t kSpinLimit = 1u << 22;
 
-// The selection (see the file comment).  state: the workspace header's
-// counter and epoch words; partial: P * k packed picks (both unused when
-// P = 1).  Every block reads the epoch the previous launch left, stores its
-// partial picks tagged with it (device scope), waits for those stores and
-// then takes a ticket from the counter.  The block with the last ticket
-// also checks that every partial slot carries the epoch (device-scope
-// loads, repeated until they do; a spin limit sets AIMA_DEVERR_TIMEOUT in
-// the error word), selects, and leaves counter 0 and the next epoch.  No
-// device-wide cache write-back or invalidate is involved (a __threadfence
-// per block made the selection take 70 us instead of a few).
+// The final selection over the P * k packed picks, FPER per thread.
+template <int FPER>
+__device__ void select_partials(const uint64_t (&w)[kPerThread], int np, int k, SelectLds& S,
+                                float* out_v, int32_t* out_i) {
+  float fv[FPER];
+  int fix[FPER];
+#pragma unroll
+  for (int j = 0; j < FPER; ++j) {
+    const int q = (int)threadIdx.x + kPassThreads * j;
+    const uint32_t i21 = (uint32_t)(w[j] >> 32) & kNoIndex21;
+    fv[j] = q < np ? __builtin_bit_cast(float, (uint32_t)w[j]) : -INFINITY;
+    fix[j] = q < np && i21 != kNoIndex21 ? (int)i21 : kNoIndex;
+  }
+  block_select<FPER>(fv, fix, k, S, out_v, out_i);
+}
+
+// The selection (see the file comment).  state: the workspace header (the
+// error word, then the launch counter at kTopkLaunchOffset); partial: P * k
+// packed picks (both unused when P = 1).  Every block reads the counter the
+// previous launch left and stores its picks tagged with this launch's epoch
+// (device-scope stores); block 0 then reads all P * k slots (device-scope
+// loads) until every one carries the epoch -- a spin limit sets
+// AIMA_DEVERR_TIMEOUT in the error word -- selects the final k and advances
+// the counter.  No block
+// waits for its own stores, takes a ticket or writes back or invalidates a
+// cache (a __threadfence per block made the selection take 70 us instead of
+// a few; a ticket counter costs every block a store and an atomic round
+// trip).  All P <= 256 blocks are resident together, so block 0's wait ends.
+template <int PER>
 __global__ __launch_bounds__(kPassThreads) void topk_kernel(
     const float* __restrict__ vals, int64_t n, int64_t chunk, int k, uint64_t* __restrict__ partial,
     uint32_t* __restrict__ state, float* __restrict__ out_v, int32_t* __restrict__ out_i) {
@@ -278,16 +335,16 @@ __global__ __launch_bounds__(kPassThreads) void topk_kernel(
   const int64_t base = (int64_t)blockIdx.x * chunk;
   const int64_t end = base + chunk < n ? base + chunk : n;
   uint32_t* const err = state;  // the workspace error word (byte 0)
-  uint32_t* const counter = state + kTopkCounterOffset / 4;
-  uint32_t* const epoch_word = counter + 1;
-  uint32_t epoch = 0;
+  uint32_t* const epoch_word = state + kTopkLaunchOffset / 4;
+  uint32_t launch = 0, epoch = 0;
   if (gridDim.x > 1) {
-    epoch = __hip_atomic_load(epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & 0x7ffu;
+    launch = __hip_atomic_load(epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    epoch = 1u + launch % 2047u;
   }
-  float v[kPerThread];
-  int ix[kPerThread];
+  float v[PER];
+  int ix[PER];
 #pragma unroll
-  for (int j = 0; j < kPerThread; ++j) {
+  for (int j = 0; j < PER; ++j) {
     // positions past the chunk read its last element (straight-line loads,
     // all in flight at once) and are then emptied
     const int64_t p = base + threadIdx.x + (int64_t)kPassThreads * j;
@@ -297,33 +354,33 @@ __global__ __launch_bounds__(kPassThreads) void topk_kernel(
     ix[j] = p < end ? (int)p : kNoIndex;
   }
   if (gridDim.x == 1) {
-    block_select<kPerThread>(v, ix, k, S, out_v, out_i);
+    block_select<PER>(v, ix, k, S, out_v, out_i);
     return;
   }
-  block_select<kPerThread>(v, ix, k, S, pick_v, pick_i);
+  block_select<PER>(v, ix, k, S, pick_v, pick_i);
   __syncthreads();
   if ((int)threadIdx.x < k) {
     __hip_atomic_store(&partial[(int64_t)blockIdx.x * k + threadIdx.x],
                        pack_pick(pick_v[threadIdx.x], pick_i[threadIdx.x], epoch),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  if (threadIdx.x == 0) {
-    // the picks are stored by lanes of this wave: let them complete first
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    S.is_last = atomicAdd(counter, 1u) == gridDim.x - 1 ? 1 : 0;
-  }
-  __syncthreads();
-  if (!S.is_last) return;
+  if (blockIdx.x != 0) return;
   const int np = (int)gridDim.x * k;  // <= 256 * 16 = 4096
   uint64_t w[kPerThread];
+  const int fper = np <= 2 * kPassThreads ? 2 : np <= 4 * kPassThreads ? 4
+                   : np <= 8 * kPassThreads ? 8 : 16;
   for (uint32_t spins = 0;; ++spins) {
     bool fresh = true;
 #pragma unroll
     for (int j = 0; j < kPerThread; ++j) {
       const int q = (int)threadIdx.x + kPassThreads * j;
-      const int qc = q < np ? q : np - 1;
-      w[j] = __hip_atomic_load(&partial[qc], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      fresh = fresh && (uint32_t)(w[j] >> 53) == epoch;
+      if (j < fper) {
+        const int qc = q < np ? q : np - 1;
+        w[j] = __hip_atomic_load(&partial[qc], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        fresh = fresh && (uint32_t)(w[j] >> 53) == epoch;
+      } else {
+        w[j] = 0;
+      }
     }
     if (__syncthreads_and(fresh)) break;
     if (spins > kSpinLimit) {
@@ -331,27 +388,30 @@ __global__ __launch_bounds__(kPassThreads) void topk_kernel(
       break;
     }
   }
-#pragma unroll
-  for (int j = 0; j < kPerThread; ++j) {
-    const int q = (int)threadIdx.x + kPassThreads * j;
-    const uint32_t i21 = (uint32_t)(w[j] >> 32) & kNoIndex21;
-    v[j] = q < np ? __builtin_bit_cast(float, (uint32_t)w[j]) : -INFINITY;
-    ix[j] = q < np && i21 != kNoIndex21 ? (int)i21 : kNoIndex;
+  if (fper == 2) {
+    select_partials<2>(w, np, k, S, out_v, out_i);
+  } else if (fper == 4) {
+    select_partials<4>(w, np, k, S, out_v, out_i);
+  } else if (fper == 8) {
+    select_partials<8>(w, np, k, S, out_v, out_i);
+  } else {
+    select_partials<16>(w, np, k, S, out_v, out_i);
   }
-  block_select<kPerThread>(v, ix, k, S, out_v, out_i);
+  // device scope, like the loads that read it: the next launch's blocks
+  // (on any XCD) must see the new counter, never this launch's
   if (threadIdx.x == 0) {
-    *counter = 0u;
-    *epoch_word = (epoch + 1u) & 0x7ffu;
+    __hip_atomic_store(epoch_word, launch + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 int partial_blocks(int64_t n) {
-  const int64_t p = (n + kPassThreads - 1) / kPassThreads;
+  const int64_t p = (n + kChunkMax - 1) / kChunkMax;
   return (int)(p < kMaxPartials ? p : kMaxPartials);
 }
 
-// Workspace: the header (error word at 0, counter and epoch at
-// kTopkCounterOffset), then the P * k packed partial picks.
+// Workspace: the header (error word at 0, launch counter at
+// kTopkLaunchOffset), then
+// the P * k packed partial picks.
 size_t topk_ws_bytes(int64_t n, int k) {
   return kWsHeader + round_up((size_t)partial_blocks(n) * k * 8, 256);
 }
@@ -368,8 +428,8 @@ int topk_launch(const float* values, int64_t n, int k, int32_t* ids, float* out_
     state = static_cast<uint32_t*>(ws);
     partial = reinterpret_cast<uint64_t*>(static_cast<char*>(ws) + kWsHeader);
   }
-  hipLaunchKernelGGL(topk_kernel, dim3((unsigned)P), dim3(kPassThreads), 0, st, values, n, chunk,
-                     k, partial, state, out_values, ids);
+  hipLaunchKernelGGL(topk_kernel<kPerThread>, dim3((unsigned)P), dim3(kPassThreads), 0, st,
+                     values, n, chunk, k, partial, state, out_values, ids);
   return launch_check("topk");
 }
 

@@ -591,14 +591,6 @@ __device__ __forceinline__ void lds_xchunk(const uint32_t* src, int w0, XChunk& 
   make_xchunk(w, c);
 }
 
-// Orders one wave's LDS writes before its following LDS reads by other lanes
-// of the same wave (a wave executes its LDS operations in order; the fences
-// keep the compiler from moving the accesses across).
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 #ifdef AIMA_DECODE_TRACE
 // Diagnostics build only (never in the product library): phase timestamps of

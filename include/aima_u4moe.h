@@ -238,11 +238,11 @@ int aima_topk_workspace_size(int64_t n, int32_t k, size_t* bytes);
  * r < k, value descending, the lower index first among equal values (the
  * order of the reference's LM-head partial top-8, q4x8_matvec.cl:973-1021).
  * NaNs are never chosen; ranks past the last number hold (-inf, 0x7fffffff).
- * n <= 1,048,576, k <= 16; the workspace may be null when n <= 1024.  One
- * launch: its blocks meet at a counter in the workspace header (bytes
- * 128..135), which must be zero when the workspace is first used (as the
- * error word must be) and which every call leaves zero; calls sharing a
- * workspace must not overlap. */
+ * n <= 1,048,576, k <= 16; the workspace may be null when n <= 4096.  One
+ * launch: each block stores its picks in the workspace tagged with a launch
+ * number kept in the workspace header (bytes 128..135; zero-fill a new
+ * workspace once, as for the error word, and every call advances it), and
+ * block 0 merges them; calls sharing a workspace must not overlap. */
 int aima_topk_f32(const float* values, int64_t n, int32_t k, int32_t* ids,
                   float* out_values, void* workspace, size_t workspace_bytes,
                   void* stream);

@@ -15,7 +15,7 @@ pytestmark = pytest.mark.gpu
 THREADS = min(16, os.cpu_count() or 1)
 
 
-@pytest.mark.parametrize("n", [1, 100, 1024, 1025, 70001, 248320, 1048576])
+@pytest.mark.parametrize("n", [1, 100, 1024, 1025, 4096, 4097, 70001, 248320, 1048576])
 @pytest.mark.parametrize("k", [1, 8, 16])
 def test_topk_matches_oracle_with_ties(pkg, dev, n, k):
     if k > n:
@@ -83,9 +83,9 @@ def test_topk_rejects_bad_sizes(pkg, dev):
 
 
 # ---------------------------------------------------------------------------
-# fused LM-head top-k: the matvec blocks append candidates at or above a
-# shared threshold, one merge block selects (the state lives in the
-# workspace header and is cleared by every call)
+# LM-head top-k: the matvec into the logits, then one selection launch whose
+# blocks each store their picks and whose block 0 merges them (the launch
+# epoch lives in the workspace header)
 # ---------------------------------------------------------------------------
 
 def _structured_head(pkg, dev, n, K, scales, group=128):
