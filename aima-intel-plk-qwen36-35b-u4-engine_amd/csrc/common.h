@@ -173,8 +173,9 @@ __device__ __forceinline__ float segment_sum(float v) {
 // DPP steps inside each 16-lane row, then the four row winners read out and
 // combined in a fixed order; the result is wave-uniform.  Every lane of the
 // wave must be active.
+// (bitwise on the comparisons: no short-circuit branches)
 __device__ __forceinline__ bool pair_better(float v, int i, float bv, int bi) {
-  return v > bv || (v == bv && i < bi);
+  return (v > bv) | ((v == bv) & (i < bi));
 }
 template <int CTRL>
 __device__ __forceinline__ void pair_step(float& bv, int& bi) {
@@ -445,7 +446,7 @@ __device__ __forceinline__ void router_select_wave(const float* __restrict__ l, 
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int i = lane + 64 * j;
-      if (i < experts && (p[j] > bp || (p[j] == bp && i < bi))) {
+      if ((i < experts) & pair_better(p[j], i, bp, bi)) {
         bp = p[j];
         bi = i;
       }

@@ -243,7 +243,7 @@ __device__ __forceinline__ int dpp_int(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
 }
 __device__ __forceinline__ bool route_better(float p, int i, float bp, int bi) {
-  return p > bp || (p == bp && i < bi);
+  return (p > bp) | ((p == bp) & (i < bi));
 }
 template <int CTRL>
 __device__ __forceinline__ void argmax_step(float& bp, int& bi) {
