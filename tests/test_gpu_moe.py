@@ -96,9 +96,13 @@ def test_decode_flags_bad_expert_id(pkg, dev, layer_small):
 # grouped schedule
 # ---------------------------------------------------------------------------
 
+# (1024, 1024, 16): the largest expert count and k, 16 chunks of 1024
+# assignments; (2049, 256, 8): a partial last chunk of 8 assignments.
 @pytest.mark.parametrize("T,E,k,zipf", [(2048, 256, 8, 1.1), (1, 256, 8, None),
                                         (37, 16, 8, None), (1000, 64, 6, None),
-                                        (16384, 256, 8, None)])
+                                        (16384, 256, 8, None), (2049, 256, 8, 1.1),
+                                        (1024, 1024, 16, 1.1), (1025, 1024, 16, None),
+                                        (3, 1024, 16, None)])
 def test_schedule_bit_exact(pkg, dev, T, E, k, zipf):
     ids, w = pkg.select_router_topk(pkg.synth.router_logits(T, E, seed=T, device=dev,
                                                             zipf_s=zipf), k)
@@ -118,6 +122,29 @@ def test_schedule_flags_errors(pkg, dev):
     ids = torch.tensor([[0, 1, 2, 8]], dtype=torch.int32, device=dev)
     pkg.build_grouped_schedule(ids, torch.ones((1, 4), device=dev), 8, ws=ws)
     assert ws.error_bits() & pkg._lib.AIMA_DEVERR_EXPERT_RANGE
+
+
+@pytest.mark.parametrize("T", [200, 3000])
+def test_schedule_flags_duplicate_across_chunks(pkg, dev, T):
+    """At k = 6, token 170 holds assignments 1020..1025, across the boundary of
+    the 1024-assignment blocks of the schedule.  A duplicate between its rank
+    0 and rank 5 (in different blocks) is flagged, with 2 blocks (T = 200) and
+    18 (T = 3000); a clean routing flags nothing and ranks as the oracle."""
+    ws = pkg.Workspace(dev)
+    g = torch.Generator(device="cpu")
+    g.manual_seed(T)
+    ids = torch.stack([torch.randperm(64, generator=g)[:6] for _ in range(T)]).to(torch.int32)
+    ids = ids.to(dev)
+    w = torch.ones((T, 6), device=dev)
+    s = pkg.build_grouped_schedule(ids, w, 64, ws=ws)
+    torch.cuda.synchronize()
+    assert ws.error_bits() == 0
+    r = oracle.build_grouped_schedule(ids.cpu().numpy(), 64, w.cpu().numpy())
+    assert np.array_equal(s["token_map"].cpu().numpy(), r["token_map"])
+    bad = ids.clone()
+    bad[170, 5] = bad[170, 0]
+    pkg.build_grouped_schedule(bad, w, 64, ws=ws)
+    assert ws.error_bits() == pkg._lib.AIMA_DEVERR_EXPERT_DUPLICATE
 
 
 # ---------------------------------------------------------------------------
