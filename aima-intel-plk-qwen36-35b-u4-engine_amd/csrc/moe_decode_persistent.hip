@@ -392,20 +392,6 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return max_u64(max_u64(readlane_u64(v, 0), readlane_u64(v, 16)),
                  max_u64(readlane_u64(v, 32), readlane_u64(v, 48)));
 }
-template <int CTRL>
-__device__ __forceinline__ double dpp_f64(double v) {
-  return __builtin_bit_cast(double, dpp_u64<CTRL>(__builtin_bit_cast(uint64_t, v)));
-}
-__device__ __forceinline__ double readlane_f64(double v, int l) {
-  return __builtin_bit_cast(double, readlane_u64(__builtin_bit_cast(uint64_t, v), l));
-}
-__device__ __forceinline__ double wave_sum_f64(double v) {
-  v += dpp_f64<0xB1>(v);
-  v += dpp_f64<0x4E>(v);
-  v += dpp_f64<0x141>(v);
-  v += dpp_f64<0x140>(v);
-  return (readlane_f64(v, 0) + readlane_f64(v, 16)) + (readlane_f64(v, 32) + readlane_f64(v, 48));
-}
 
 // Lane r <= k returns the expert id of rank r by the 32-bit key (-1 past
 // the finite logits).  A lane keeps its four keys sorted; a round is one
@@ -446,7 +432,10 @@ __device__ int rank_logits(const float (&v)[4], int experts, int k) {
   return mine;
 }
 
-// f32 probabilities of the softmax (f64 exp and sum); -inf past `experts`
+// f32 probabilities of the softmax (f64 exp and sum); -inf past `experts`.
+// The f64 sum runs in select_router_topk's order (lane partials over t, then
+// an xor butterfly), so the probabilities, and the weights made from them,
+// are bit-identical to that kernel's.
 __device__ void softmax_probs(const float (&v)[4], int experts, float (&p)[4]) {
   const int lane = threadIdx.x & 63;
   float mx = -INFINITY;
@@ -466,7 +455,8 @@ __device__ void softmax_probs(const float (&v)[4], int experts, float (&p)[4]) {
     e[t] = lane + 64 * t < experts ? exp((double)v[t] - (double)mx) : 0.0;
     sum += e[t];
   }
-  sum = wave_sum_f64(sum);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
 #pragma unroll
   for (int t = 0; t < 4; ++t) p[t] = lane + 64 * t < experts ? (float)(e[t] / sum) : -INFINITY;
 }
@@ -547,6 +537,30 @@ __device__ bool route_confirm(const float (&p)[4], int experts, int rank_id, int
   }
   out_w = rank_weight(pr, k, min_sum);
   return ok;
+}
+
+// One layer's route from its logits (experts <= 256, one wave): the ranking
+// of the logits, confirmed against the probabilities (or replaced by their
+// own ranking), as the routed plan does per layer.  Lane r < k gets rank r.
+__device__ void route_layer_ranked(const float* __restrict__ l, int experts, int k, float min_sum,
+                                   int32_t* id, float* w) {
+  const int lane = threadIdx.x & 63;
+  float lv[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int i = lane + 64 * t;
+    lv[t] = i < experts ? l[i] : -INFINITY;
+  }
+  int rid = rank_logits(lv, experts, k);
+  if (lane > k) rid = -1;
+  float pv[4];
+  softmax_probs(lv, experts, pv);
+  float rw = 0.f;
+  if (!route_confirm(pv, experts, rid, k, min_sum, rw)) select_probs(pv, experts, k, min_sum, rid, rw);
+  if (lane < k) {
+    *id = rid;
+    *w = rw;
+  }
 }
 
 __device__ __forceinline__ uint32_t h2bits(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
@@ -669,7 +683,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   __syncthreads();
 
   auto local_route = [&](int L, int32_t* id, float* w) {
-    if (a.logits) {
+    if (a.logits && a.experts <= kRouterRows) {
+      route_layer_ranked(a.logits + (int64_t)L * a.experts, a.experts, k, a.min_weight_sum, id, w);
+    } else if (a.logits) {
       route_layer(a.logits + (int64_t)L * a.experts, a.experts, k, a.min_weight_sum, id, w);
     } else if (lane < k) {
       *id = a.ids_in[L * k + lane];

@@ -255,6 +255,30 @@ def test_decode_plan_small_stack(pkg, dev):
         assert_parity(f16_to_f32(a), oracle.f16_values(ref[0]), what=f"plan small rep={rep}")
 
 
+@pytest.mark.parametrize("k", [8, 3])
+def test_decode_plan_routes_match_select_router_topk(pkg, dev, k):
+    """At 256 experts the plan ranks each layer's logits in its prologue and
+    confirms the ranking on the probabilities; the result must be the
+    routes of select_router_topk bit for bit: the plan run from logits
+    equals the plan run on select_router_topk's ids and weights, also with
+    tied logits (4 distinct values repeated) and with a run of equal top
+    logits, where the probability ranking decides."""
+    layers = make_stack(pkg, dev, 3, 2048, 512, 256, seed=1300 + k)
+    plan = pkg.DecodePlan(layers, k=k)
+    x = pkg.synth.activations(1, 2048, 1310 + k, dev)[0]
+    base = torch.stack([pkg.synth.router_logits(1, 256, 1320 + k + l, dev)[0] for l in range(3)])
+    tied = base.clone()
+    tied[1] = base[1, torch.arange(256, device=dev) % 4]
+    tied[2, 17:27] = tied[2].max() + 0.5
+    for logits in (base, tied):
+        ids, w = pkg.select_router_topk(logits, k)
+        a = plan.run(x, router_logits=logits)
+        b = plan.run(x, ids=ids, weights=w)
+        torch.cuda.synchronize()
+        assert plan.error_bits() == 0
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("k", [1, 4])
 def test_decode_plan_small_k(pkg, dev, k):
     """Fewer than 8 routed experts: the XCDs of the missing ranks compute only
