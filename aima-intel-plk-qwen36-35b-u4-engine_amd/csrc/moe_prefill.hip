@@ -473,12 +473,15 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
     u32x4 q0, q1;    // 64 nibbles: k 64 hh .. +64 of the group
     uint32_t s, z;   // f16 scale bits, zero-point byte
   };
+  // Global loads by address space: the gate/up row pointers are picked per
+  // lane from a two-entry table, through which the compiler loses the
+  // address space (flat loads would also count against the LDS counter).
   auto load_w = [&](int g) {
     WGroup r;
-    r.q0 = *reinterpret_cast<const u32x4*>(t.wq + g * 64);
-    r.q1 = *reinterpret_cast<const u32x4*>(t.wq + g * 64 + 16);
-    r.s = t.ws[g];
-    r.z = t.wz[(t.zbase + g) >> 1];
+    r.q0 = gload16(t.wq + g * 64);
+    r.q1 = gload16(t.wq + g * 64 + 16);
+    r.s = ((const AIMA_GLOBAL uint16_t*)t.ws)[g];
+    r.z = ((const AIMA_GLOBAL uint8_t*)t.wz)[(t.zbase + g) >> 1];
     return r;
   };
 
