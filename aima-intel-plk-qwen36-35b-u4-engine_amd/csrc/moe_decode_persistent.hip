@@ -657,12 +657,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   AIMA_TRACE(40, 0, 0);  // kernel entry
 
   if (threadIdx.x == 0) S.abort = 0;
-  {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.layers);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(S.table);
-    const int words = a.n_layers * (int)(sizeof(PlanLayer) / 4);
-    for (int i = threadIdx.x; i < words; i += kThreads) dst[i] = src[i];
-  }
   // block 0 advances the launch counter on every exit path
   auto finish = [&]() {
     if (b == 0 && threadIdx.x == 0) *a.epoch_counter = *a.epoch_counter + 1u;
@@ -680,7 +674,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     finish();
     return;
   }
-  __syncthreads();
 
   auto local_route = [&](int L, int32_t* id, float* w) {
     if (a.logits && a.experts <= kRouterRows) {
@@ -693,8 +686,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     }
   };
   // ---- prologue --------------------------------------------------------------
-  // Block L computes and publishes layer L's route (wave 0); then every block
-  // reads all routes into LDS (one wave per layer, in parallel).
+  // Block L computes and publishes layer L's route (wave 0) while the other
+  // waves copy the layer table into LDS; then every block reads all routes
+  // into LDS (one wave per layer, in parallel).
   if (!ROUTED && wave == 0) {
     for (int L = b; L < a.n_layers; L += nb) {
       int32_t id = 0;
@@ -707,6 +701,16 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       }
     }
   }
+  {
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.layers);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(S.table);
+    const int words = a.n_layers * (int)(sizeof(PlanLayer) / 4);
+    const int first = ROUTED ? 0 : 64;  // wave 0 routes in the logits-fed plan
+    for (int i = (int)threadIdx.x - first; i >= 0 && i < words; i += kThreads - first) {
+      dst[i] = src[i];
+    }
+  }
+  __syncthreads();
   // lane l of wave w reads slot l & 7 of layer L0 + w + 8 (l >> 3)
   for (int L0 = 0; !ROUTED && L0 < a.n_layers; L0 += 8 * kWaves) {
     const int L = L0 + wave + kWaves * (lane >> 3);
