@@ -608,12 +608,13 @@ __device__ __forceinline__ void lds_xchunk(const uint32_t* src, int w0, XChunk& 
 
 #ifdef AIMA_DECODE_TRACE
 // Diagnostics build only (never in the product library): phase timestamps of
-// every block, 100 MHz real-time clock, g_trace[(L * 256 + block) * 16 + slot].
+// every block, 100 MHz real-time clock, g_trace[(L * 256 + block) * 32 + slot];
+// row 40 (the prologue) keeps the block's hardware XCD id in slot 31.
 __device__ uint64_t* g_trace = nullptr;
 #define AIMA_TRACE(L, slot, T)                                              \
   do {                                                                      \
     if (trace && threadIdx.x == (T) && b < 256)                             \
-      trace[((L) * 256 + b) * 16 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+      trace[((L) * 256 + b) * 32 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
 #else
 #define AIMA_TRACE(L, slot, T) \
@@ -655,6 +656,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   uint64_t* const trace = g_trace;
 #endif
   AIMA_TRACE(40, 0, 0);  // kernel entry
+#ifdef AIMA_DECODE_TRACE
+  if (trace && threadIdx.x == 0 && b < 256) trace[(40 * 256 + b) * 32 + 31] = (uint64_t)x;
+#endif
 
   if (threadIdx.x == 0) S.abort = 0;
   // block 0 advances the launch counter on every exit path
@@ -931,7 +935,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
   // loads leave back to back (the loaders above read the table per row,
   // which the prefetch interleaved with the dot products can afford; a burst
   // that starts when the route is known cannot).  Same rows, lanes and
-  // clamping as prefetch_a, gather_a, prefetch_b and gather_b.
+  // clamping as prefetch_a, gather_a, prefetch_b and gather_b, but the
+  // gate/up rows go straight into the working registers, the gathering load
+  // first: each dot product then waits for its own row only (take_gather_a
+  // hands the scale and zero-point words out once the gather has landed).
+  // The down rows go to the prefetch registers (rotate_b at barrier #4).
   auto issue_rows = [&](int L) {
     const int ln = opaque_v(threadIdx.x & 63);
     const PlanLayer& T = S.table[L];
@@ -948,22 +956,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     const AIMA_GLOBAL uint8_t* dsc = uptr(T.ds) + (size_t)e * ((uint32_t)kH * gB * 2);
     const AIMA_GLOBAL uint8_t* dzp = uptr(T.dz) + (size_t)e * ((uint32_t)kH * gB / 2);
     const AIMA_GLOBAL uint8_t *sw = uptr(T.sdq), *ssc = uptr(T.sds), *szp = uptr(T.sdz);
-    // gate/up rows
-#pragma unroll
-    for (int i = 0; i < kMaxRowsA; ++i) {
-      const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
-      const bool h = (ri & 1) != 0;
-      const int p = j * kPairs + (ri >> 1);
-      const bool routed = p < kI;
-      const int unit = routed ? p : x * kSlice + (p - kI);
-      wa_n[i] = ld_w(routed ? (h ? rq1 : rq0) : (h ? hq1 : hq0),
-                     (uint32_t)unit * (kH / 2) + ln * 16);
-      if (!g128) {
-        const int gi = unit * gA + ((ln * 32) >> glog2);
-        sa_n[i] = ld_u32(routed ? (h ? rs1 : rs0) : (h ? hs1 : hs0), (gi * 2) & ~3);
-        za_n[i] = ld_u32(routed ? (h ? rz1 : rz0) : (h ? hz1 : hz0), (gi >> 1) & ~3);
-      }
-    }
     if (g128) {
       const int q = min(ln, 49);
       const bool is_s = q < 40;
@@ -979,6 +971,22 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
                : (routed ? (up ? rz1 : rz0) : (up ? hz1 : hz0));
       const uint32_t off = is_s ? (uint32_t)unit * 32 + 4 * w : (uint32_t)unit * 8 + 4 * w;
       gsa_n = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
+    }
+    // gate/up rows
+#pragma unroll
+    for (int i = 0; i < kMaxRowsA; ++i) {
+      const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
+      const bool h = (ri & 1) != 0;
+      const int p = j * kPairs + (ri >> 1);
+      const bool routed = p < kI;
+      const int unit = routed ? p : x * kSlice + (p - kI);
+      wa[i] = ld_w(routed ? (h ? rq1 : rq0) : (h ? hq1 : hq0),
+                   (uint32_t)unit * (kH / 2) + ln * 16);
+      if (!g128) {
+        const int gi = unit * gA + ((ln * 32) >> glog2);
+        sa[i] = ld_u32(routed ? (h ? rs1 : rs0) : (h ? hs1 : hs0), (gi * 2) & ~3);
+        za[i] = ld_u32(routed ? (h ? rz1 : rz0) : (h ? hz1 : hz0), (gi >> 1) & ~3);
+      }
     }
     // down rows
     const int h0 = j * kRowsB + wave * kWaveRowsB;
@@ -1057,6 +1065,18 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       }
     }
   };
+  // Routed plan: the gathered gate/up scale and zero-point words to their
+  // lanes (the rows themselves were loaded in place).
+  auto take_gather_a = [&]() {
+    const int ln = opaque_v(threadIdx.x & 63);
+    if (g128) {
+#pragma unroll
+      for (int i = 0; i < kMaxRowsA; ++i) {
+        sa[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((8 * i + (ln >> 3)) * 4, (int)gsa_n);
+        za[i] = (uint32_t)__builtin_amdgcn_ds_bpermute((40 + 2 * i + (ln >> 5)) * 4, (int)gsa_n);
+      }
+    }
+  };
   auto rotate_b = [&]() {
     const int ln = opaque_v(threadIdx.x & 63);
 #pragma unroll
@@ -1081,6 +1101,32 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       for (int u = 0; u < 3; ++u) {
         sb[u] = sb_n[u];
         zb[u] = zb_n[u];
+      }
+    }
+  };
+  // Phase A's dot products: the block's 36 gate/up rows against the
+  // operands in xc, row sums to LDS.  The logits-fed plan loads one row of
+  // the next layer per dot product (held in place by a scheduling barrier);
+  // the routed plan has no prefetch to pace, so every slot is computed (a
+  // surplus one on the clamped row it loaded, result dropped) and the five
+  // dot products can interleave.
+  auto dots_a = [&](const XChunk& xc, int L) {
+    const int ln = opaque_v(threadIdx.x & 63);
+#pragma unroll
+    for (int i = 0; i < kMaxRowsA; ++i) {
+      const int ri = ((wave + 4) & 7) + kWaves * i;
+      if (!ROUTED) {
+        if (L + 1 < a.n_layers) prefetch_a1(S.table[L + 1], slot_expert(L + 1), i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (ROUTED || ri < kRowsA) {
+        const int rc = min(ri, kRowsA - 1);
+        const int p = j * kPairs + (rc >> 1);
+        const int unit = p < kI ? p : x * kSlice + (p - kI);
+        const int gi = unit * gA + ((ln * 32) >> glog2);
+        const float dd =
+            segment_sum<64>(u4_chunk_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
+        if ((threadIdx.x & 63) == 0 && ri < kRowsA) S.rowsum[ri] = dd;
       }
     }
   };
@@ -1245,8 +1291,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
             const int rank_id = rank_logits(lv, a.experts, k);
             if (ln <= k) S.rank[ln] = rank_id;
             if (ln < k) S.route_id[L][ln] = rank_id;
+            AIMA_TRACE(L, 16, 0);  // ranked (wave 0)
           } else {
             softmax_probs(lv, a.experts, pv);
+            AIMA_TRACE(L, 17, 64);  // probabilities (wave 1)
           }
         }
         __syncthreads();  // #2b: the layer's route by the ranking
@@ -1255,13 +1303,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
           finish();
           return;
         }
-        // the layer's gate/up and down rows from that route (wave 1 first
-        // checks it: an issue into a full memory queue would hold the check
-        // behind the loads)
-        if (wave != 1) {
-          issue_rows(L);
-          AIMA_TRACE(L, 14, 128);  // loads issued (wave 2)
-        } else {
+        // every wave issues the layer's gate/up and down rows from that
+        // ranking; wave 1 then checks it while the loads are in flight (a
+        // changed route is loaded again after barrier #3)
+        issue_rows(L);
+        AIMA_TRACE(L, 14, 128);  // loads issued (wave 2)
+        AIMA_TRACE(L, 18, 64);   // loads issued (wave 1)
+        if (wave == 1) {
           int id = ln <= k ? S.rank[ln] : -1;
           float w = 0.f;
           const bool same = route_confirm(pv, a.experts, id, k, a.min_weight_sum, w);
@@ -1272,42 +1320,20 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
               atomicOr(a.err, AIMA_DEVERR_EXPERT_RANGE);
               id = -1;
             }
-            S.route_id[L][ln] = id;
+            // (the ranking's ids stand unless the route changed; the other
+            // waves may be reading them for their loads)
+            if (!same) S.route_id[L][ln] = id;
             S.route_w[L][ln] = w;
             if (b == 0 && a.ids_out) a.ids_out[L * k + ln] = id;
             if (b == 0 && a.w_out) a.w_out[L * k + ln] = w;
           }
           if (ln == 0) S.reroute = same ? 0 : 1;
           AIMA_TRACE(L, 15, 64);  // route confirmed (wave 1)
-          wave_lds_sync();
-          issue_rows(L);
         }
-        __syncthreads();  // #2c: the layer's final route
-        AIMA_TRACE(L, 13, 0);
-        if (S.reroute) issue_rows(L);
-        rotate_a();
+        take_gather_a();
+        AIMA_TRACE(L, 19, 256);  // gate/up scales in registers (wave 4)
       }
-#pragma unroll
-      for (int i = 0; i < kMaxRowsA; ++i) {
-        const int ri = ((wave + 4) & 7) + kWaves * i;
-        if (!ROUTED) {
-          // one row of the next layer per dot product (kept in place)
-          if (L + 1 < a.n_layers) prefetch_a1(S.table[L + 1], slot_expert(L + 1), i);
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        // The routed plan has no prefetch to pace: every slot is computed
-        // (a surplus one on the clamped row it loaded, result dropped) so the
-        // dot products of the five rows can interleave.
-        if (ROUTED || ri < kRowsA) {
-          const int rc = min(ri, kRowsA - 1);
-          const int p = j * kPairs + (rc >> 1);
-          const int unit = p < kI ? p : x * kSlice + (p - kI);
-          const int gi = unit * gA + ((ln * 32) >> glog2);
-          const float dd =
-              segment_sum<64>(u4_chunk_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
-          if (lane == 0 && ri < kRowsA) S.rowsum[ri] = dd;
-        }
-      }
+      dots_a(xc, L);
     }
     if (wave == 0) {
       // shared-expert gate sigma = sigmoid(gate_vec . x), per block
@@ -1321,6 +1347,16 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     }
     AIMA_TRACE(L, 3, 256);  // A dots done (wave 4)
     __syncthreads();  // #3: row sums ready
+    if (ROUTED && S.reroute) {
+      // the probabilities did not confirm the ranking (ties or near ties):
+      // the confirmed route's rows, and the dot products again
+      issue_rows(L);
+      take_gather_a();
+      XChunk xc;
+      get_chunk(S.xa_p, S.xa_bias, S.xa_xsum, ln, xc);
+      dots_a(xc, L);
+      __syncthreads();  // #3r: row sums of the confirmed route
+    }
     AIMA_TRACE(L, 4, 0);
     if (wave == 0) {
       // SwiGLU for the block's 18 pairs, published three per record
@@ -1388,6 +1424,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
         prefetch_router(L + 1);
       }
       rotate_b();
+      AIMA_TRACE(L, 20, 0);  // down rows in registers (wave 0)
     }
     // ================= phase B_L =================
     {

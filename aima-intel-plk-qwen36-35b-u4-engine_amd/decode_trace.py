@@ -42,14 +42,18 @@ ROUTED_PHASES = [(0, 1, "r_L read -> barrier #1"),
                  (1, 2, "#1 -> #2 (RMSNorm, operands)"),
                  (2, 11, "#2 -> XCD logits read (router dot + hop)"),
                  (11, 12, "logits read -> #2b (ranking)"),
+                 (11, 16, "  logits read -> ranked (wave 0)"),
+                 (11, 17, "  logits read -> probabilities (wave 1)"),
                  (12, 14, "#2b -> routed rows issued (wave 2)"),
+                 (12, 18, "#2b -> routed rows issued (wave 1)"),
                  (12, 15, "#2b -> route confirmed (wave 1)"),
-                 (12, 13, "#2b -> #2c"),
-                 (13, 3, "#2c -> gate/up dots done (wave 4)"),
+                 (12, 19, "#2b -> gate/up rows in registers (wave 4)"),
+                 (12, 3, "#2b -> gate/up dots done (wave 4)"),
                  (3, 4, "dots -> #3"),
                  (4, 5, "#3 -> activations published"),
                  (5, 6, "act published -> XCD act read (hop)"),
                  (6, 7, "act read -> #4 (staging)"),
+                 (7, 20, "  #4 -> down rows in registers (wave 0)"),
                  (7, 8, "#4 -> P published (down dots)"),
                  (8, 9, "P published -> P read (cross-XCD hop)"),
                  (9, 10, "P read -> r_{L+1} rows stored (relay)")]
@@ -88,13 +92,15 @@ def main():
     torch.cuda.synchronize()
     plan.check()
     lib.aima_debug_set_decode_trace.argtypes = [C.c_void_p]
-    tr = torch.zeros(41 * 256 * 16, dtype=torch.int64, device=dev)
+    tr = torch.zeros(41 * 256 * 32, dtype=torch.int64, device=dev)
     pkg._lib.check(lib.aima_debug_set_decode_trace(tr.data_ptr()), "set decode trace")
     for _ in range(3):
         run()
     torch.cuda.synchronize()
     plan.check()
-    A = tr.cpu().numpy().reshape(41, 256, 16).astype(np.float64) * 10.0  # ns
+    raw = tr.cpu().numpy().reshape(41, 256, 32)
+    xcd = raw[40, :, 31].copy()  # the hardware XCD id of every block
+    A = raw.astype(np.float64) * 10.0  # ns
 
     def st(v):
         v = np.asarray(v)
@@ -110,6 +116,28 @@ def main():
                                                      for l in range(2, 38)]))))
     hop = [A[l, :, 0] - A[l - 1, :, 10].max() for l in range(2, 38)]
     print("%-44s %s" % ("last r_L store -> r_L read (residual hop)", st(np.concatenate(hop))))
+    # The hops measured from the last stamp a reader depends on (block b is
+    # rank b / 8 of the XCD it recorded): the act hop waits for the 32 blocks
+    # of its XCD, the relay of rank j for rank j of every XCD, the layer
+    # start for the 32 relays of its XCD.
+    j_of = np.arange(256) // 8
+
+    def by_xcd(v):
+        return np.array([v[xcd == xcd[b]].max() for b in range(256)])
+
+    def by_rank(v):
+        return np.array([v[j_of == j_of[b]].max() for b in range(256)])
+
+    act_src = [by_xcd(A[l, :, 5]) for l in range(2, 38)]
+    p_src = [by_rank(A[l, :, 8]) for l in range(2, 38)]
+    r_src = [by_xcd(A[l - 1, :, 10]) for l in range(2, 38)]
+    for name, s, dst in [("last XCD act published -> act read", act_src, 6),
+                         ("last P of the rank published -> P read", p_src, 9)]:
+        print("%-44s %s" % (name, st(np.concatenate([A[l, :, dst] - s[i]
+                                                       for i, l in enumerate(range(2, 38))]))))
+    print("%-44s %s" % ("last XCD relay store -> r_L read",
+                        st(np.concatenate([A[l, :, 0] - r_src[i]
+                                           for i, l in enumerate(range(2, 38))]))))
     lay = [A[l + 1, :, 0] - A[l, :, 0] for l in range(2, 38)]
     print("%-44s %s" % ("layer (r_L read -> r_{L+1} read)", st(np.concatenate(lay))))
 
