@@ -474,8 +474,8 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
     uint32_t s, z;   // f16 scale bits, zero-point byte
   };
   // Global loads by address space: the gate/up row pointers are picked per
-  // lane from a two-entry table, through which the compiler loses the
-  // address space (flat loads would also count against the LDS counter).
+  // lane (gate or up tensor), through which the compiler loses the address
+  // space (flat loads would also count against the LDS counter).
   auto load_w = [&](int g) {
     WGroup r;
     r.q0 = gload16(t.wq + g * 64);
@@ -682,9 +682,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
       const int h = q >> 1;
       const int64_t j = (int64_t)t.ntile * 128 + wave * 16 + 8 * (q & 1) + (i & 7);
       wrow = V.row(eoff, h, j);
-      wq = V.q[h];
-      ws = V.s[h];
-      wz = V.z[h];
+      // selects, not V.q[h]: indexing the view with a per-lane h puts it in
+      // scratch memory, and every tile's first weight loads then wait for a
+      // scratch store and load
+      wq = h ? V.q[1] : V.q[0];
+      ws = h ? V.s[1] : V.s[0];
+      wz = h ? V.z[1] : V.z[0];
     } else {
       const aima_u4_tensor& W = routed_tile ? L.down : L.shared_down;
       wrow = eoff * H + (int64_t)t.ntile * 256 + wave * 32 + i;
