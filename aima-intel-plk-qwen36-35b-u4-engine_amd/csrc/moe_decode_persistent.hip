@@ -98,7 +98,7 @@ struct PlanLayer {
   const uint8_t* dq;
   const uint16_t* ds;
   const uint8_t* dz;
-  const uint8_t* sdq;
+  const uint8_t* sdq;             // shared down, slice-major copy [xcd][kH][32 B]
   const uint16_t* sds;
   const uint8_t* sdz;
   const uint16_t* gate_vec;
@@ -930,7 +930,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       const int row = h0 + ((ln & 15) >> 1);
       const int ch = 2 * x + (ln & 1);
       const int gi = row * gB + ((ch * 32) >> glog2);
-      wb_n[2] = ld_w(uptr(Ly.sdq), (uint32_t)row * (kI / 2) + ch * 16);
+      wb_n[2] = ld_w(uptr(Ly.sdq), (uint32_t)x * (kH * 32) + row * 32 + (ln & 1) * 16);
       if (!g128) {
         sb_n[2] = ld_u32(uptr(Ly.sds), (gi * 2) & ~3);
         zb_n[2] = ld_u32(uptr(Ly.sdz), (gi >> 1) & ~3);
@@ -1012,7 +1012,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     {
       const int row = h0 + ((ln & 15) >> 1);
       const int ch = 2 * x + (ln & 1);
-      wb_n[2] = ld_w(sw, (uint32_t)row * (kI / 2) + ch * 16);
+      wb_n[2] = ld_w(sw, (uint32_t)x * (kH * 32) + row * 32 + (ln & 1) * 16);
       if (!g128) {
         const int gi = row * gB + ((ch * 32) >> glog2);
         sb_n[2] = ld_u32(ssc, (gi * 2) & ~3);
@@ -1688,6 +1688,11 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   const size_t o_rw = take(sizeof(uint64_t) * n_layers * k);
   const size_t o_lgx = take(sizeof(uint64_t) * kXcds * 2 * kRouterRows);
   const size_t o_ctr = take(256);
+  // each layer's shared-expert down weights, slice-major: XCD x reads K
+  // slice x (32 bytes) of every row, which the row-major tensor spreads
+  // over a 128-byte line per row (4x the bytes through the L2)
+  constexpr size_t kSliceBytes = (size_t)kH * (kI / 2);
+  const size_t o_sdq = take(kSliceBytes * n_layers);
   aima_moe_decode_plan* p = new aima_moe_decode_plan();
   p->device = dev;
   p->n_layers = n_layers;
@@ -1712,9 +1717,19 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   e = hipMemset(p->mem, 0, off);
   if (e == hipSuccess) {
     p->host.resize(n_layers);
-    for (int l = 0; l < n_layers; ++l) p->host[l] = plan_layer(layers[l]);
-    e = hipMemcpy(p->table, p->host.data(), sizeof(PlanLayer) * n_layers,
-                  hipMemcpyHostToDevice);
+    for (int l = 0; l < n_layers && e == hipSuccess; ++l) {
+      p->host[l] = plan_layer(layers[l]);
+      char* dst = p->mem + o_sdq + kSliceBytes * l;
+      for (int xs = 0; xs < kXcds && e == hipSuccess; ++xs) {
+        e = hipMemcpy2D(dst + (size_t)xs * kH * 32, 32, layers[l].shared_down.qweight + xs * 32,
+                        kI / 2, 32, kH, hipMemcpyDeviceToDevice);
+      }
+      p->host[l].sdq = reinterpret_cast<const uint8_t*>(dst);
+    }
+    if (e == hipSuccess) {
+      e = hipMemcpy(p->table, p->host.data(), sizeof(PlanLayer) * n_layers,
+                    hipMemcpyHostToDevice);
+    }
   }
   if (e != hipSuccess) {
     (void)hipFree(p->mem);

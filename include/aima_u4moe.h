@@ -496,7 +496,10 @@ int aima_moe_stack_decode_routed_noalloc(const aima_moe_layer* layers,
  * moe_decode_persistent.hip).  create() validates the shapes, checks that
  * the device has 256 CUs (8 XCDs x 32) and keeps one 512-thread block
  * resident on each, allocates the plan's
- * device buffers and uploads the layer table (synchronous, setup time only;
+ * device buffers, uploads the layer table and copies each layer's
+ * shared-expert down weights into an XCD-slice-major layout (512 KB per
+ * layer; the plan reads that copy, so changed shared-down weights need a
+ * new plan) (synchronous, setup time only;
  * AIMA_E_UNSUPPORTED when the shape or device does not fit, in which case
  * aima_moe_stack_decode is the general path).  run() is asynchronous,
  * allocates nothing and can be captured in a HIP graph: routing comes from
