@@ -86,6 +86,9 @@ def lib():
         L.orc_moe_ffn_decode_threaded.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p,
                                                   C.c_void_p, C.c_void_p, _i64,
                                                   C.c_void_p, _i64]
+        L.orc_moe_ffn_tokens_model.argtypes = [C.c_void_p, _i64, C.c_void_p, C.c_void_p,
+                                               C.c_void_p, C.c_void_p, _i64, C.c_int,
+                                               C.c_void_p, _i64]
         L.orc_build_grouped_schedule.argtypes = [_i32p, _i64, _i64, _i64, _f32p, _i32p,
                                                  _i32p, _i32p, _f32p, C.c_void_p,
                                                  C.c_void_p]
@@ -516,6 +519,70 @@ def moe_ffn_decode_threaded(mw: MoeWeights, x, ids, w, residual=None,
     del keep
     _check(rc, "moe_ffn_decode_threaded")
     return out
+
+
+# Precision models (u4moe_oracle.c, orc_moe_ffn_tokens_model): the same layer
+# with other rounding points and summation orders, used only to measure how
+# far two correct implementations of a layer stack drift apart through the
+# f16 residual.  Never a parity reference.
+MODEL_ACT_F16 = 1       # SwiGLU rounded to f16 before the down matvec
+MODEL_SLICED = 2        # persistent decode order: sum over x of (w_x d_x + sigma shared_x)
+MODEL_CHUNKED = 4       # dot products as 32-element chunk sums + pairwise tree
+MODEL_WEIGHT_F16 = 8    # dequantized weights rounded to f16 (prefill MFMA operand)
+MODEL_CONTRIB_F16 = 16  # prefill combine: f16 contribution rows, fma with sigma
+MODEL_F64 = 32          # f64 arithmetic (exact up to the f16 h and r roundings)
+MODEL_DECODE_PLAN = MODEL_ACT_F16 | MODEL_SLICED | MODEL_CHUNKED
+MODEL_PREFILL = MODEL_ACT_F16 | MODEL_CHUNKED | MODEL_WEIGHT_F16 | MODEL_CONTRIB_F16
+
+
+def moe_ffn_tokens_model(mw: MoeWeights, x, ids, w, residual=None, flags: int = 0,
+                         threads: int = 8) -> np.ndarray:
+    """moe_ffn_tokens under a precision model (flags = 0: bit-identical)."""
+    x = _f32(x)
+    T = x.shape[0]
+    ids = np.ascontiguousarray(ids, np.int32)
+    w = _f32(w)
+    res = None if residual is None else _f32(residual)
+    out = np.empty((T, mw.hidden), np.float32)
+    cs, keep = mw._c()
+    rc = lib().orc_moe_ffn_tokens_model(C.addressof(cs), T, x.ctypes.data,
+                                        None if res is None else res.ctypes.data,
+                                        ids.ctypes.data, w.ctypes.data, ids.shape[1], int(flags),
+                                        out.ctypes.data, threads)
+    del keep
+    _check(rc, "moe_ffn_tokens_model")
+    return out
+
+
+def rms_norm_rows_model(x, weight, eps: float, flags: int = 0) -> np.ndarray:
+    """RMSNorm under a precision model: flags = 0 is rms_norm_rows; with
+    MODEL_F64 the sum of squares and scaling are f64; with MODEL_CHUNKED the
+    sum of squares is numpy's pairwise f32 sum (another f32 order)."""
+    x = _f32(x)
+    if not flags & (MODEL_F64 | MODEL_CHUNKED):
+        return rms_norm_rows(x, weight, eps)
+    wt = _f32(weight).reshape(-1)
+    if flags & MODEL_F64:
+        xd = x.astype(np.float64)
+        scale = 1.0 / np.sqrt(np.mean(xd * xd, axis=-1, keepdims=True) + eps)
+        return (xd * scale * wt.astype(np.float64)).astype(np.float32)
+    ss = np.sum(x * x, axis=-1, keepdims=True, dtype=np.float32)
+    scale = np.float32(1.0) / np.sqrt(ss / np.float32(x.shape[-1]) + np.float32(eps))
+    return ((x * scale) * wt).astype(np.float32)
+
+
+def moe_stack_chain_model(layers, norm_weights, x0_bits, ids, w, eps: float = 1e-6,
+                          flags: int = 0, threads: int = 8):
+    """moe_stack_tokens' chain under a precision model: per layer
+    h = f16(rms_norm(r)), r = f16(r + ffn(h)).  Returns the last r (f16 bits)."""
+    r = np.ascontiguousarray(x0_bits, np.uint16)
+    for L, mw in enumerate(layers):
+        rf = f16_values(r)
+        h = f16_values(float_to_half(rms_norm_rows_model(rf, norm_weights[L], eps, flags))
+                       .reshape(rf.shape))
+        o = moe_ffn_tokens_model(mw, h, ids[L], w[L], residual=rf, flags=flags, threads=threads)
+        r = float_to_half(o).reshape(o.shape)
+    return r
 
 
 def build_grouped_schedule(ids, experts: int, router_weights=None) -> dict:

@@ -807,3 +807,231 @@ int orc_build_grouped_schedule(const int32_t* ids, int64_t tokens, int64_t k,
   free(cursors);
   return rc;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Precision models of the stack (TEST INFRASTRUCTURE, not a parity          */
+/* reference).  They recompute one layer with the rounding points and        */
+/* summation orders of other correct implementations, so that a test can    */
+/* measure how far two implementations of the 40-layer stack drift apart     */
+/* through the f16 residual alone (the floor any end-to-end comparison with  */
+/* the reference's order sits on).  Flags:                                   */
+/*   ORC_MODEL_ACT_F16     SwiGLU outputs (routed and shared) rounded to f16 */
+/*                         before the down matvec (the device operand)       */
+/*   ORC_MODEL_SLICED      the persistent decode's order: P_x = w_x * d_x +  */
+/*                         sigma * shared_down[:, slice x](act), x = 0..7,   */
+/*                         out = residual + (P_0 + ... + P_7)                */
+/*   ORC_MODEL_CHUNKED     every dot product as 32-element f32 chunk sums    */
+/*                         combined by a pairwise tree (a different f32      */
+/*                         order, like the device's lane partial sums)       */
+/*   ORC_MODEL_WEIGHT_F16  dequantized weights rounded to f16 (the grouped   */
+/*                         prefill's MFMA operand)                           */
+/*   ORC_MODEL_CONTRIB_F16 the grouped prefill's combine: routed rows        */
+/*                         f16(w_r * d_r), shared row f16(d_sh), f32 rank-   */
+/*                         order sum, fma(shared, sigma, sum) + residual     */
+/*   ORC_MODEL_F64         dot products, SwiGLU, weighting and sums in f64   */
+/*                         (exact arithmetic up to the stack's own f16 h and */
+/*                         r roundings)                                      */
+/* With flags = 0 the result equals orc_moe_ffn_tokens bit for bit.          */
+/* ------------------------------------------------------------------------ */
+
+#define ORC_MODEL_ACT_F16 1
+#define ORC_MODEL_SLICED 2
+#define ORC_MODEL_CHUNKED 4
+#define ORC_MODEL_WEIGHT_F16 8
+#define ORC_MODEL_CONTRIB_F16 16
+#define ORC_MODEL_F64 32
+
+static double model_dot(const float* w, const double* x, int64_t n, int flags) {
+  if (flags & ORC_MODEL_F64) {
+    double s = 0.0;
+    for (int64_t i = 0; i < n; ++i) s += (double)w[i] * x[i];
+    return s;
+  }
+  if (flags & ORC_MODEL_CHUNKED) {
+    float part[512];
+    int64_t m = 0;
+    for (int64_t c = 0; c < n; c += 32, ++m) {
+      float s = 0.0f;
+      for (int64_t i = c; i < c + 32 && i < n; ++i) s += w[i] * (float)x[i];
+      part[m] = s;
+    }
+    while (m > 1) {
+      int64_t h = (m + 1) / 2;
+      for (int64_t i = 0; i < m / 2; ++i) part[i] = part[2 * i] + part[2 * i + 1];
+      if (m & 1) part[m / 2] = part[m - 1];
+      m = h;
+    }
+    return part[0];
+  }
+  float s = 0.0f;
+  for (int64_t i = 0; i < n; ++i) s += w[i] * (float)x[i];
+  return s;
+}
+
+static void model_row(const orc_u4_tensor* t, int64_t expert, int64_t row,
+                      int flags, float* out) {
+  const int64_t groups = t->k / t->group;
+  const uint8_t* qw = t->qweight + expert * t->rows * (t->k / 2);
+  const uint16_t* sc = t->scale + expert * t->rows * groups;
+  const uint8_t* zp = t->zp + expert * (t->rows * groups / 2);
+  for (int64_t k = 0; k < t->k; ++k) {
+    float w = u4_weight(qw, sc, zp, row, k, t->k, groups, t->group);
+    if (flags & ORC_MODEL_WEIGHT_F16) w = orc_half_to_float(orc_float_to_half(w));
+    out[k] = w;
+  }
+}
+
+static double model_swiglu(double g, double u, int flags) {
+  const double s = g >= 0.0 ? 1.0 / (1.0 + exp(-g)) : exp(g) / (1.0 + exp(g));
+  if (flags & ORC_MODEL_F64) return g * s * u;
+  float a = (float)(g * s * u);
+  if (flags & ORC_MODEL_ACT_F16) a = orc_half_to_float(orc_float_to_half(a));
+  return a;
+}
+
+/* gate/up, SwiGLU and down of one expert: act [inter], d [hidden].  Values
+ * are kept as double but hold f32 numbers unless ORC_MODEL_F64. */
+static void model_expert(const orc_u4_tensor* gu, const orc_u4_tensor* dn,
+                         int64_t e, const double* x, int flags, float* row,
+                         double* act, double* d) {
+  const int64_t I = gu->rows / 2, H = dn->rows;
+  for (int64_t i = 0; i < I; ++i) {
+    model_row(gu, e, i, flags, row);
+    const double g = model_dot(row, x, gu->k, flags);
+    model_row(gu, e, I + i, flags, row);
+    const double u = model_dot(row, x, gu->k, flags);
+    act[i] = model_swiglu(g, u, flags);
+  }
+  for (int64_t h = 0; h < H; ++h) {
+    model_row(dn, e, h, flags, row);
+    d[h] = model_dot(row, act, dn->k, flags);
+  }
+}
+
+static int model_token(const orc_moe_weights* mw, const float* xf,
+                       const float* residual, const int32_t* ids,
+                       const float* w, int64_t k, int flags, float* out) {
+  const int64_t H = mw->hidden, I = mw->inter, IS = mw->shared_inter;
+  const int f64 = flags & ORC_MODEL_F64;
+  for (int64_t r = 0; r < k; ++r) {
+    if (ids[r] < 0 || ids[r] >= mw->gate_up.experts) return ORC_ERANGE;
+  }
+  int64_t kmax = H > I ? H : I;
+  if (IS > kmax) kmax = IS;
+  double* x = (double*)malloc(sizeof(double) * (size_t)H);
+  float* row = (float*)malloc(sizeof(float) * (size_t)kmax);
+  double* act = (double*)malloc(sizeof(double) * (size_t)(I > IS ? I : IS));
+  double* d = (double*)malloc(sizeof(double) * (size_t)(k * H));
+  double* dsh = (double*)malloc(sizeof(double) * (size_t)H);
+  double* shs = (double*)malloc(sizeof(double) * (size_t)(8 * H));
+  if (!x || !row || !act || !d || !dsh || !shs) {
+    free(x); free(row); free(act); free(d); free(dsh); free(shs);
+    return ORC_ERUNTIME;
+  }
+  for (int64_t i = 0; i < H; ++i) x[i] = xf[i];
+  for (int64_t r = 0; r < k; ++r) {
+    model_expert(&mw->gate_up, &mw->down, ids[r], x, flags, row, act, d + r * H);
+  }
+  /* shared expert: gate/up + SwiGLU, then its down matvec whole or per slice */
+  for (int64_t i = 0; i < IS; ++i) {
+    model_row(&mw->shared_gate_up, 0, i, flags, row);
+    const double g = model_dot(row, x, H, flags);
+    model_row(&mw->shared_gate_up, 0, IS + i, flags, row);
+    const double u = model_dot(row, x, H, flags);
+    if (f64) {
+      act[i] = model_swiglu(g, u, flags);
+    } else {
+      /* the shared expert's f32 form (orc_swiglu_pair) */
+      float a = (float)g * orc_sigmoid_scalar((float)g) * (float)u;
+      if (flags & ORC_MODEL_ACT_F16) a = orc_half_to_float(orc_float_to_half(a));
+      act[i] = a;
+    }
+  }
+  const int64_t sl = IS / 8;
+  for (int64_t h = 0; h < H; ++h) {
+    model_row(&mw->shared_down, 0, h, flags, row);
+    dsh[h] = model_dot(row, act, IS, flags);
+    if ((flags & ORC_MODEL_SLICED) && sl > 0) {
+      for (int64_t s = 0; s < 8; ++s) shs[s * H + h] = model_dot(row + s * sl, act + s * sl, sl, flags);
+    }
+  }
+  double gsum = 0.0;
+  float gf = 0.0f;
+  for (int64_t i = 0; i < H; ++i) {
+    gsum += (double)mw->shared_gate_vec[i] * x[i];
+    gf += mw->shared_gate_vec[i] * xf[i];
+  }
+  const double sig = f64 ? (gsum >= 0.0 ? 1.0 / (1.0 + exp(-gsum)) : exp(gsum) / (1.0 + exp(gsum)))
+                         : (double)orc_sigmoid_scalar(gf);
+  for (int64_t h = 0; h < H; ++h) {
+    const float res = residual ? residual[h] : 0.0f;
+    if (f64) {
+      double moe = 0.0;
+      for (int64_t r = 0; r < k; ++r) moe += d[r * H + h] * (double)w[r];
+      out[h] = (float)((double)res + (moe + dsh[h] * sig));
+    } else if ((flags & ORC_MODEL_SLICED) && sl > 0) {
+      float s = 0.0f;
+      for (int64_t q = 0; q < 8; ++q) {
+        float p = (float)sig * (float)shs[q * H + h];
+        if (q < k) p = fmaf(w[q], (float)d[q * H + h], p);
+        s += p;
+      }
+      out[h] = res + s;
+    } else if (flags & ORC_MODEL_CONTRIB_F16) {
+      float s = 0.0f;
+      for (int64_t r = 0; r < k; ++r) {
+        s += orc_half_to_float(orc_float_to_half((float)d[r * H + h] * w[r]));
+      }
+      const float o = fmaf(orc_half_to_float(orc_float_to_half((float)dsh[h])), (float)sig, s);
+      out[h] = res + o;
+    } else {
+      float moe = 0.0f;
+      for (int64_t r = 0; r < k; ++r) moe += (float)d[r * H + h] * w[r];
+      const float ffn = moe + (float)dsh[h] * (float)sig;
+      out[h] = residual ? res + ffn : ffn;
+    }
+  }
+  free(x); free(row); free(act); free(d); free(dsh); free(shs);
+  return ORC_OK;
+}
+
+typedef struct {
+  const orc_moe_weights* mw;
+  const float* x;
+  const float* residual;
+  const int32_t* ids;
+  const float* w;
+  int64_t k;
+  int flags;
+  float* out;
+  int rc;
+  pthread_mutex_t lock;
+} model_ctx;
+
+static void model_range(void* p, int64_t begin, int64_t end) {
+  model_ctx* c = (model_ctx*)p;
+  const int64_t H = c->mw->hidden;
+  for (int64_t t = begin; t < end; ++t) {
+    const int rc = model_token(c->mw, c->x + t * H, c->residual ? c->residual + t * H : NULL,
+                               c->ids + t * c->k, c->w + t * c->k, c->k, c->flags,
+                               c->out + t * H);
+    if (rc != ORC_OK) {
+      pthread_mutex_lock(&c->lock);
+      if (c->rc == ORC_OK) c->rc = rc;
+      pthread_mutex_unlock(&c->lock);
+      return;
+    }
+  }
+}
+
+int orc_moe_ffn_tokens_model(const orc_moe_weights* mw, int64_t tokens,
+                             const float* x, const float* residual,
+                             const int32_t* ids, const float* w, int64_t k,
+                             int flags, float* out, int64_t threads) {
+  if (!moe_weights_ok(mw) || k <= 0 || k > 64 || tokens < 0) return ORC_EINVAL;
+  if (mw->hidden > 16384 || mw->inter > 16384 || mw->shared_inter > 16384) return ORC_EINVAL;
+  if ((flags & ORC_MODEL_SLICED) && (k > 8 || mw->shared_inter % 8 != 0)) return ORC_EINVAL;
+  model_ctx c = {mw, x, residual, ids, w, k, flags, out, ORC_OK, PTHREAD_MUTEX_INITIALIZER};
+  orc_parallel_for_rows(tokens, threads, model_range, &c);
+  return c.rc;
+}

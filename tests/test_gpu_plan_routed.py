@@ -194,7 +194,7 @@ def test_config4a_routed_plan_40_layers(pkg, dev, stack40r):
     """The headline shape with true decode: 40 layers x 256 experts, k = 8.
     Every layer's selection exact on its logits and equal to the logits-fed
     plan on the same routes; logits of the first 3 layers against the
-    oracle's FC (later layers follow from the same kernel code)."""
+    oracle's FC; the fused launch equal to 40 chained 1-layer launches."""
     layers, routers = stack40r
     plan = pkg.DecodePlan(layers, k=8, routers=routers)
     x = pkg.synth.activations(1, 2048, 4141, dev)[0].contiguous()
@@ -209,3 +209,17 @@ def test_config4a_routed_plan_40_layers(pkg, dev, stack40r):
     ids = routes.expert_ids.cpu().numpy()
     assert ((ids >= 0) & (ids < 256)).all()
     assert all(len(set(row)) == 8 for row in ids)
+    # the 40-layer launch equals 40 chained 1-layer routed launches fed their
+    # own outputs, routes and logits included, bit for bit
+    chained = x
+    for l in range(40):
+        one = pkg.DecodePlan([layers[l]], k=8, routers=[routers[l]])
+        rl = one.route_buffers()
+        chained = one.run(chained, routers=[routers[l]], route_out=rl)
+        torch.cuda.synchronize()
+        assert one.error_bits() == 0
+        assert torch.equal(rl.expert_ids[0], routes.expert_ids[l]), l
+        assert torch.equal(rl.weights[0], routes.weights[l]), l
+        assert torch.equal(rl.logits[0], routes.logits[l]), l
+        one.close()
+    assert torch.equal(chained, out), "40-layer routed plan differs from chained 1-layer plans"
