@@ -10,7 +10,7 @@
 // owns a contiguous chunk of at most 4096 values (16 per thread) and selects
 // its k best (block_select) into its partial slots.  Block 0 then selects
 // the final k from the P * k partials once every slot carries the launch's
-// epoch (see topk_kernel).  P = 1 writes the result directly.
+// tags (see topk_kernel).  P = 1 writes the result directly.
 // n <= 1,048,576.
 //
 // The LM head (aima_u4_lm_head_topk) is the U4 matvec into the caller's
@@ -47,10 +47,12 @@ static_assert(kRowBests >= kTopkMax, "the threshold needs k row bests");
 constexpr int kMaxCand = 256;  // candidates one wave selects from (4 per lane)
 
 // The selection's launch counter, kept in the workspace header at byte 132
-// (the error word is at 0; bytes 128..131 stay zero): any start value, so a
-// zero-filled workspace works, and it advances by one per launch.  A launch
-// tags its picks with 1 + counter % 2047, never 0, so a zero-filled slot is
-// never taken for one written by this launch.
+// (the error word is at 0; bytes 128..131 stay zero): any start value, and
+// it advances by one per launch.  A launch tags both words of each of its
+// picks with the full 32-bit counter value (see pick_value_word), so a slot
+// is taken only when it was written by this launch: a zero-filled slot, a
+// slot of an earlier launch and data other entry points left in the same
+// memory all fail the check (short of matching two 32-bit tags at once).
 constexpr size_t kTopkLaunchOffset = 132;
 
 // (bitwise on the comparisons: no short-circuit branches)
@@ -287,38 +289,42 @@ __device__ void block_select(float (&v)[PER], int (&ix)[PER], int k, SelectLds& 
   }
 }
 
-// A partial pick as one 64-bit word: the value's bits, then 21 bits of
-// index (0x1fffff = none) and 11 bits of the launch's epoch, so a reader
-// can tell a slot written by this launch from a stale one.
-constexpr uint32_t kNoIndex21 = 0x1fffffu;
-__device__ __forceinline__ uint64_t pack_pick(float v, int ix, uint32_t epoch) {
-  const uint32_t i21 = ix == kNoIndex ? kNoIndex21 : (uint32_t)ix;
-  return (uint64_t)__builtin_bit_cast(uint32_t, v) | ((uint64_t)(i21 | (epoch << 21)) << 32);
+// A partial pick as two 64-bit words, each stored and loaded whole: the
+// value's bits with the launch number, and the index with the launch number
+// xor kTagMix.  Each word validates itself; a slot is fresh when both carry
+// this launch's tags.  (kTagMix is non-zero, so an all-zero slot never
+// passes, whatever the counter.)
+constexpr uint32_t kTagMix = 0x5bd1e995u;
+__device__ __forceinline__ uint64_t pick_value_word(float v, uint32_t launch) {
+  return (uint64_t)__builtin_bit_cast(uint32_t, v) | ((uint64_t)launch << 32);
+}
+__device__ __forceinline__ uint64_t pick_index_word(int ix, uint32_t launch) {
+  return (uint64_t)(uint32_t)ix | ((uint64_t)(launch ^ kTagMix) << 32);
 }
 constexpr uint32_t kSpinLimit = 1u << 22;
 
 // The final selection over the P * k packed picks, FPER per thread.
 template <int FPER>
-__device__ void select_partials(const uint64_t (&w)[kPerThread], int np, int k, SelectLds& S,
+__device__ void select_partials(const uint64_t (&wv)[kPerThread],
+                                const uint64_t (&wi)[kPerThread], int np, int k, SelectLds& S,
                                 float* out_v, int32_t* out_i) {
   float fv[FPER];
   int fix[FPER];
 #pragma unroll
   for (int j = 0; j < FPER; ++j) {
     const int q = (int)threadIdx.x + kPassThreads * j;
-    const uint32_t i21 = (uint32_t)(w[j] >> 32) & kNoIndex21;
-    fv[j] = q < np ? __builtin_bit_cast(float, (uint32_t)w[j]) : -INFINITY;
-    fix[j] = q < np && i21 != kNoIndex21 ? (int)i21 : kNoIndex;
+    fv[j] = q < np ? __builtin_bit_cast(float, (uint32_t)wv[j]) : -INFINITY;
+    fix[j] = q < np ? (int)(uint32_t)wi[j] : kNoIndex;
   }
   block_select<FPER>(fv, fix, k, S, out_v, out_i);
 }
 
 // The selection (see the file comment).  state: the workspace header (the
 // error word, then the launch counter at kTopkLaunchOffset); partial: P * k
-// packed picks (both unused when P = 1).  Every block reads the counter the
-// previous launch left and stores its picks tagged with this launch's epoch
+// picks of two words each (both unused when P = 1).  Every block reads the
+// counter the previous launch left and stores its picks tagged with it
 // (device-scope stores); block 0 then reads all P * k slots (device-scope
-// loads) until every one carries the epoch -- a spin limit sets
+// loads) until every word carries this launch's tag -- a spin limit sets
 // AIMA_DEVERR_TIMEOUT in the error word -- selects the final k and advances
 // the counter.  No block
 // waits for its own stores, takes a ticket or writes back or invalidates a
@@ -336,10 +342,9 @@ __global__ __launch_bounds__(kPassThreads) void topk_kernel(
   const int64_t end = base + chunk < n ? base + chunk : n;
   uint32_t* const err = state;  // the workspace error word (byte 0)
   uint32_t* const epoch_word = state + kTopkLaunchOffset / 4;
-  uint32_t launch = 0, epoch = 0;
+  uint32_t launch = 0;
   if (gridDim.x > 1) {
     launch = __hip_atomic_load(epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    epoch = 1u + launch % 2047u;
   }
   float v[PER];
   int ix[PER];
@@ -360,13 +365,16 @@ __global__ __launch_bounds__(kPassThreads) void topk_kernel(
   block_select<PER>(v, ix, k, S, pick_v, pick_i);
   __syncthreads();
   if ((int)threadIdx.x < k) {
-    __hip_atomic_store(&partial[(int64_t)blockIdx.x * k + threadIdx.x],
-                       pack_pick(pick_v[threadIdx.x], pick_i[threadIdx.x], epoch),
+    uint64_t* slot = partial + 2 * ((int64_t)blockIdx.x * k + threadIdx.x);
+    __hip_atomic_store(slot, pick_value_word(pick_v[threadIdx.x], launch), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(slot + 1, pick_index_word(pick_i[threadIdx.x], launch),
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (blockIdx.x != 0) return;
   const int np = (int)gridDim.x * k;  // <= 256 * 16 = 4096
-  uint64_t w[kPerThread];
+  const uint32_t tag_i = launch ^ kTagMix;
+  uint64_t wv[kPerThread], wi[kPerThread];
   const int fper = np <= 2 * kPassThreads ? 2 : np <= 4 * kPassThreads ? 4
                    : np <= 8 * kPassThreads ? 8 : 16;
   for (uint32_t spins = 0;; ++spins) {
@@ -376,10 +384,13 @@ __global__ __launch_bounds__(kPassThreads) void topk_kernel(
       const int q = (int)threadIdx.x + kPassThreads * j;
       if (j < fper) {
         const int qc = q < np ? q : np - 1;
-        w[j] = __hip_atomic_load(&partial[qc], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        fresh = fresh && (uint32_t)(w[j] >> 53) == epoch;
+        wv[j] = __hip_atomic_load(&partial[2 * qc], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wi[j] = __hip_atomic_load(&partial[2 * qc + 1], __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        fresh = fresh && (uint32_t)(wv[j] >> 32) == launch && (uint32_t)(wi[j] >> 32) == tag_i;
       } else {
-        w[j] = 0;
+        wv[j] = 0;
+        wi[j] = 0;
       }
     }
     if (__syncthreads_and(fresh)) break;
@@ -389,13 +400,13 @@ __global__ __launch_bounds__(kPassThreads) void topk_kernel(
     }
   }
   if (fper == 2) {
-    select_partials<2>(w, np, k, S, out_v, out_i);
+    select_partials<2>(wv, wi, np, k, S, out_v, out_i);
   } else if (fper == 4) {
-    select_partials<4>(w, np, k, S, out_v, out_i);
+    select_partials<4>(wv, wi, np, k, S, out_v, out_i);
   } else if (fper == 8) {
-    select_partials<8>(w, np, k, S, out_v, out_i);
+    select_partials<8>(wv, wi, np, k, S, out_v, out_i);
   } else {
-    select_partials<16>(w, np, k, S, out_v, out_i);
+    select_partials<16>(wv, wi, np, k, S, out_v, out_i);
   }
   // device scope, like the loads that read it: the next launch's blocks
   // (on any XCD) must see the new counter, never this launch's
@@ -410,10 +421,9 @@ int partial_blocks(int64_t n) {
 }
 
 // Workspace: the header (error word at 0, launch counter at
-// kTopkLaunchOffset), then
-// the P * k packed partial picks.
+// kTopkLaunchOffset), then the P * k partial picks, 16 bytes each.
 size_t topk_ws_bytes(int64_t n, int k) {
-  return kWsHeader + round_up((size_t)partial_blocks(n) * k * 8, 256);
+  return kWsHeader + round_up((size_t)partial_blocks(n) * k * 16, 256);
 }
 
 int topk_launch(const float* values, int64_t n, int k, int32_t* ids, float* out_values, void* ws,

@@ -83,15 +83,19 @@ class Workspace:
 
 
 _default_ws: dict = {}
+# the device top-k keeps its launch counter and picks in its own workspace
+# (other entry points' data never sits under its pick slots)
+_default_topk_ws: dict = {}
 
 
-def _ws(ws: Optional[Workspace], device) -> Workspace:
+def _ws(ws: Optional[Workspace], device, pool: Optional[dict] = None) -> Workspace:
     if ws is not None:
         return ws
+    pool = _default_ws if pool is None else pool
     key = str(device)
-    if key not in _default_ws:
-        _default_ws[key] = Workspace(device)
-    return _default_ws[key]
+    if key not in pool:
+        pool[key] = Workspace(device)
+    return pool[key]
 
 
 # ---------------------------------------------------------------------------
@@ -288,7 +292,7 @@ def topk_f32(values: torch.Tensor, k: int, ws: Optional[Workspace] = None):
     if values.dtype != torch.float32 or values.dim() != 1 or not values.is_contiguous():
         raise ValueError("values must be a contiguous float32 vector")
     n = values.numel()
-    ws = _ws(ws, values.device)
+    ws = _ws(ws, values.device, _default_topk_ws)
     buf = ws.get(size_query("aima_topk_workspace_size", n, int(k)))
     ids = torch.empty(int(k), dtype=torch.int32, device=values.device)
     out = torch.empty(int(k), dtype=torch.float32, device=values.device)
@@ -304,7 +308,7 @@ def lm_head_topk(x: torch.Tensor, w: U4Weight, k: int = 8, ws: Optional[Workspac
     if x.dtype != torch.float16 or x.numel() != w.k or not x.is_contiguous():
         raise ValueError("x must be a contiguous float16 vector of length k")
     n = w.experts * w.rows
-    ws = _ws(ws, x.device)
+    ws = _ws(ws, x.device, _default_topk_ws)
     buf = ws.get(size_query("aima_topk_workspace_size", n, int(k)))
     logits = torch.empty(n, dtype=torch.float32, device=x.device)
     ids = torch.empty(int(k), dtype=torch.int32, device=x.device)

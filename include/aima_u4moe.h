@@ -239,10 +239,12 @@ int aima_topk_workspace_size(int64_t n, int32_t k, size_t* bytes);
  * order of the reference's LM-head partial top-8, q4x8_matvec.cl:973-1021).
  * NaNs are never chosen; ranks past the last number hold (-inf, 0x7fffffff).
  * n <= 1,048,576, k <= 16; the workspace may be null when n <= 4096.  One
- * launch: each block stores its picks in the workspace tagged with a launch
- * number kept in the workspace header (bytes 128..135; zero-fill a new
- * workspace once, as for the error word, and every call advances it), and
- * block 0 merges them; calls sharing a workspace must not overlap. */
+ * launch: each block stores its picks in the workspace, both 64-bit words of
+ * each tagged with a 32-bit launch number kept in the workspace header
+ * (bytes 132..135: any start value, every call advances it), and block 0
+ * merges them once every word carries this launch's tag, so whatever the
+ * pick region held before (zeros, earlier picks, other entry points' data)
+ * is never taken for a pick.  Calls sharing a workspace must not overlap. */
 int aima_topk_f32(const float* values, int64_t n, int32_t k, int32_t* ids,
                   float* out_values, void* workspace, size_t workspace_bytes,
                   void* stream);
@@ -484,7 +486,9 @@ int aima_moe_stack_decode_routed(const aima_moe_layer* layers,
  * inter <= 2048, k <= 16); a shape past 128 KiB would return
  * AIMA_E_UNSUPPORTED.  Every call on one GPU shares that
  * GPU's array: calls that overlap on one GPU (other streams, other threads)
- * race and must be serialized by the caller. */
+ * race and must be serialized by the caller.  The first call on each device
+ * resolves the array's device address (hipGetSymbolAddress, once per device):
+ * make that call outside graph capture; later calls may be captured. */
 int aima_moe_stack_decode_routed_noalloc(const aima_moe_layer* layers,
                                          const aima_u4_tensor* routers, int32_t n_layers,
                                          float eps, const uint16_t* residual_in, int32_t k,

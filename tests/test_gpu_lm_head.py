@@ -170,10 +170,11 @@ def test_lm_head_topk_zero_logits_tie(pkg, dev):
     assert (vals == 0).all()
 
 
-def test_lm_head_topk_state_cleared_between_calls(pkg, dev):
-    """The selection state in the workspace header is left zero by every
-    call: back-to-back calls with different inputs, a different k, and other
-    entry points using the same workspace in between all select exactly."""
+def test_lm_head_topk_state_reused_between_calls(pkg, dev):
+    """The workspace keeps a launch counter that every call advances, and the
+    picks it leaves behind stay in place: back-to-back calls with different
+    inputs, a different k, and top-k calls of another size on the same
+    workspace in between all select exactly."""
     ws = pkg.Workspace(dev)
     gen = pkg.synth.generator(11, dev)
     w = pkg.synth.u4_weight(1, 248320, 2048, 128, gen, dev)
@@ -185,4 +186,46 @@ def test_lm_head_topk_state_cleared_between_calls(pkg, dev):
         torch.cuda.synchronize()
         ref_i, _ = oracle.lm_head_topk(v.cpu().numpy(), 8)
         assert np.array_equal(ids.cpu().numpy(), ref_i)
+    assert ws.error_bits() == 0
+
+
+def _s64(v: int) -> int:
+    """A 64-bit pattern as the signed value torch.int64 holds."""
+    v &= (1 << 64) - 1
+    return v - (1 << 64) if v >= (1 << 63) else v
+
+
+def test_lm_head_topk_foreign_data_in_pick_region(pkg, dev):
+    """A pick is taken only when both of its words carry this launch's 32-bit
+    tags, whatever the pick region held before the call: a real MoE decode's
+    data written through the same workspace, words that carry the next
+    launch's 11-bit epoch in bits 53..63 (what a one-word, 11-bit tag would
+    have accepted), and value words carrying the next launch's full tag
+    next to index words that do not."""
+    ws = pkg.Workspace(dev)
+    gen = pkg.synth.generator(12, dev)
+    w = pkg.synth.u4_weight(1, 248320, 2048, 128, gen, dev)
+    layer = pkg.synth.moe_layer(hidden=2048, inter=512, experts=16, seed=13, device=dev)
+    need = max(pkg.ops.size_query("aima_topk_workspace_size", 248320, 16), 1 << 20)
+    buf = ws.get(need)
+    g = torch.Generator(device=dev)
+    g.manual_seed(14)
+    for rep, k in enumerate((8, 16, 8, 4)):
+        h = pkg.synth.activations(1, 2048, 20 + rep, dev)[0]
+        ids = torch.randperm(16, device=dev)[:8].to(torch.int32)
+        wts = torch.full((8,), 0.125, device=dev)
+        pkg.run_moe_ffn_layer(layer, h, ids, wts, residual=h, ws=ws)  # foreign data
+        torch.cuda.synchronize()
+        buf = ws.buf
+        launch = int(buf[132:136].view(torch.int32).item()) & 0xffffffff
+        words = buf[256:].view(torch.int64)
+        low = torch.randint(0, 1 << 30, (words.numel(),), generator=g, device=dev)
+        epoch11 = _s64((1 + launch % 2047) << 53)
+        if rep == 1:
+            words.copy_(low | epoch11)
+        elif rep == 2:
+            words.copy_(low | epoch11)
+            words[0::2] = low[0::2] | _s64(launch << 32)
+        x = pkg.synth.activations(1, 2048, 30 + rep, dev)[0]
+        _check_head(pkg, dev, w, x, k, ws=ws)
     assert ws.error_bits() == 0
