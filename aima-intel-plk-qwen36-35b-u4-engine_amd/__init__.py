@@ -26,6 +26,7 @@ from .ops import (  # noqa: F401
     matvec_u4,
     matvec_u4_multi,
     moe_decode_down,
+    moe_3gemm_fused_compressed,
     moe_decode_gate_up,
     moe_stack_decode,
     moe_stack_decode_routed,

@@ -53,12 +53,12 @@ class MoeLayerC(C.Structure):
 
 class PrefillOptionsC(C.Structure):
     _fields_ = [("output_mode", _i32), ("input_f32", _i32), ("topk_stride", _i64),
-                ("stage_events", _vp * 5)]
+                ("stage_events", _vp * 5), ("swiglu_f32", _vp), ("contributions_f32", _vp)]
 
 
 class PrefillViewsC(C.Structure):
     _fields_ = [("offsets", _vp), ("token_map", _vp), ("inverse_map", _vp),
-                ("compact_weights", _vp), ("weighted_swiglu", _vp), ("contributions", _vp),
+                ("compact_weights", _vp), ("swiglu", _vp), ("contributions", _vp),
                 ("tiles", _vp), ("tile_count", _vp)]
 
 
@@ -108,6 +108,9 @@ SIGNATURES = {
                                            C.c_size_t, _vp]),
     "aima_moe_grouped_prefill_ex": (C.c_int, [_LP, _vp, _vp, _i64, _vp, _vp, _i32, _vp,
                                               C.POINTER(PrefillOptionsC), _vp, C.c_size_t, _vp]),
+    "aima_moe_grouped_prefill_logits": (C.c_int, [_LP, _vp, _vp, _i64, _vp, _i32, _f32, _vp,
+                                                  _vp, _vp, C.POINTER(PrefillOptionsC), _vp,
+                                                  C.c_size_t, _vp]),
     "aima_moe_prefill_workspace_views": (C.c_int, [_LP, _i64, _i32, _vp,
                                                    C.POINTER(PrefillViewsC)]),
     "aima_grouped_schedule_workspace_size": (C.c_int, [_i64, _i32, _i32, _szp]),

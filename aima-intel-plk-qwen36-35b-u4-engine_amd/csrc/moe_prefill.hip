@@ -428,7 +428,7 @@ __device__ __forceinline__ void plain_barrier() {
 constexpr int kGemmThreads = 512;
 constexpr int kStageA = kBM * 128 * 2;   // token rows of one group, bytes
 constexpr int kSmemBytes = 2 * kStageA;  // two-buffer ring; the epilogue reuses it
-constexpr int kSmemWeights = kSmemBytes;  // gate/up: router weights of the tile rows (1 KB)
+constexpr int kSmemWeights = kSmemBytes;  // down: router weights of the tile rows (1 KB)
 
 struct GemmTile {
   const void* a_base;     // token rows (uniform)
@@ -449,12 +449,22 @@ __device__ __forceinline__ float silu_mul_fast(float g, float u) {
   return g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
 }
 
+// Optional f32 copies of the GEMM outputs (RunLayer's grouped_swiglu_f32 /
+// grouped_contributions_f32, grouped_s8_u4_prefill_runtime.hpp:101-107): the
+// SwiGLU rows and the weighted down rows before their f16 rounding, in
+// schedule order (null: not written).
+struct GemmCapture {
+  float* act32;      // [rows][I]
+  float* contrib32;  // [rows][H]
+};
+
 template <bool GATEUP, int MB>
 __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
                                           const aima_moe_layer& L,
                                           const float* __restrict__ row_weight,
                                           uint16_t* __restrict__ act_out,
-                                          uint16_t* __restrict__ contrib_out) {
+                                          uint16_t* __restrict__ contrib_out,
+                                          const GemmCapture& cap) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int n = lane & 31, hh = lane >> 5;
@@ -490,10 +500,10 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x16{};
   const uint32_t magic = u4_magic();
 
-  // gate/up: the tile rows' router weights go to LDS with the first loads
+  // down: the tile rows' router weights go to LDS with the first loads
   // (waves 0-3, one row per lane; rows past the tile read the first row)
   const bool routed = t.e < t.E;
-  if (GATEUP && routed && wave < kBM / 64) {
+  if (!GATEUP && routed && wave < kBM / 64) {
     const int r = wave * 64 + lane;
     lds_load4(uniform_ptr(row_weight), (uint32_t)((t.row0 + (r < t.rows ? r : 0)) * 4),
               lds0 + (uint32_t)(kSmemWeights + wave * 256));
@@ -588,13 +598,17 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
   const int64_t H = L.hidden, I = L.inter;
   constexpr int kChunks = GATEUP ? 16 : 32;   // 16-byte chunks per tile row
   constexpr int kRowBytes = kChunks * 16;
-  // gate/up scales the activations by the router weight (the down
-  // projection is linear, so its output is the weighted contribution)
+  // The reference's order (grouped_s8_u4_f16_contribution_moe.cl:627-683):
+  // gate/up stores the SwiGLU rows unweighted; down multiplies its output by
+  // the row's router weight (shared-expert rows: 1; the combine applies the
+  // sigmoid gate).  Lane (n, hh) of block mb owns columns
+  // 8 (wave * Q + q) + 4 hh .. +3 of token row m = 32 mb + n.
   float wt[MB];
   const float* s_wt = reinterpret_cast<const float*>(smem + kSmemWeights);
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) wt[mb] = (GATEUP && routed) ? s_wt[mb * 32 + n] : 1.0f;
+  for (int mb = 0; mb < MB; ++mb) wt[mb] = (!GATEUP && routed) ? s_wt[mb * 32 + n] : 1.0f;
   __syncthreads();  // every wave is done with the token-row buffers
+  const int64_t col_base = (int64_t)t.ntile * (GATEUP ? 128 : 256) + hh * 4;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int m = mb * 32 + n;
@@ -602,22 +616,34 @@ __device__ __forceinline__ void gemm_tile(const GemmTile& t, uint8_t* smem,
     if (GATEUP) {
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
+        float a[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) a[c] = silu_mul_fast(acc[mb][4 * q + c], acc[mb][8 + 4 * q + c]);
         u32x2 v;
-        v.x = pack_h2(wt[mb] * silu_mul_fast(acc[mb][4 * q + 0], acc[mb][8 + 4 * q + 0]),
-                      wt[mb] * silu_mul_fast(acc[mb][4 * q + 1], acc[mb][8 + 4 * q + 1]));
-        v.y = pack_h2(wt[mb] * silu_mul_fast(acc[mb][4 * q + 2], acc[mb][8 + 4 * q + 2]),
-                      wt[mb] * silu_mul_fast(acc[mb][4 * q + 3], acc[mb][8 + 4 * q + 3]));
+        v.x = pack_h2(a[0], a[1]);
+        v.y = pack_h2(a[2], a[3]);
         const int chunk = (wave * 2 + q) ^ (m & (kChunks - 1));
         *reinterpret_cast<u32x2*>(rowp + chunk * 16 + hh * 8) = v;
+        if (cap.act32 && m < t.rows) {
+          *reinterpret_cast<float4*>(cap.act32 + (t.row0 + m) * I + col_base + (wave * 2 + q) * 8) =
+              make_float4(a[0], a[1], a[2], a[3]);
+        }
       }
     } else {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
+        float o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = wt[mb] * acc[mb][4 * q + c];
         u32x2 v;
-        v.x = pack_h2(acc[mb][4 * q + 0], acc[mb][4 * q + 1]);
-        v.y = pack_h2(acc[mb][4 * q + 2], acc[mb][4 * q + 3]);
+        v.x = pack_h2(o[0], o[1]);
+        v.y = pack_h2(o[2], o[3]);
         const int chunk = (wave * 4 + q) ^ (m & (kChunks - 1));
         *reinterpret_cast<u32x2*>(rowp + chunk * 16 + hh * 8) = v;
+        if (cap.contrib32 && m < t.rows) {
+          *reinterpret_cast<float4*>(cap.contrib32 + (t.row0 + m) * H + col_base + (wave * 4 + q) * 8) =
+              make_float4(o[0], o[1], o[2], o[3]);
+        }
       }
     }
   }
@@ -645,7 +671,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
     aima_moe_layer L, const uint16_t* __restrict__ src, const int32_t* __restrict__ tiles,
     const int32_t* __restrict__ tile_count, const int32_t* __restrict__ token_map,
     const float* __restrict__ row_weight, int64_t A, int ntiles_n,
-    uint16_t* __restrict__ act_out, uint16_t* __restrict__ contrib_out) {
+    uint16_t* __restrict__ act_out, uint16_t* __restrict__ contrib_out, GemmCapture cap) {
   __shared__ __attribute__((aligned(1024))) uint8_t smem[kSmemBytes + kBM * 4];
   const int p = blockIdx.x;
   const int slot = p >> 3;
@@ -718,14 +744,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(
   }
 
   switch ((t.rows + 31) >> 5) {
-    case 1: gemm_tile<GATEUP, 1>(t, smem, L, row_weight, act_out, contrib_out); break;
-    case 2: gemm_tile<GATEUP, 2>(t, smem, L, row_weight, act_out, contrib_out); break;
-    case 3: gemm_tile<GATEUP, 3>(t, smem, L, row_weight, act_out, contrib_out); break;
-    case 4: gemm_tile<GATEUP, 4>(t, smem, L, row_weight, act_out, contrib_out); break;
-    case 5: gemm_tile<GATEUP, 5>(t, smem, L, row_weight, act_out, contrib_out); break;
-    case 6: gemm_tile<GATEUP, 6>(t, smem, L, row_weight, act_out, contrib_out); break;
-    case 7: gemm_tile<GATEUP, 7>(t, smem, L, row_weight, act_out, contrib_out); break;
-    default: gemm_tile<GATEUP, 8>(t, smem, L, row_weight, act_out, contrib_out); break;
+    case 1: gemm_tile<GATEUP, 1>(t, smem, L, row_weight, act_out, contrib_out, cap); break;
+    case 2: gemm_tile<GATEUP, 2>(t, smem, L, row_weight, act_out, contrib_out, cap); break;
+    case 3: gemm_tile<GATEUP, 3>(t, smem, L, row_weight, act_out, contrib_out, cap); break;
+    case 4: gemm_tile<GATEUP, 4>(t, smem, L, row_weight, act_out, contrib_out, cap); break;
+    case 5: gemm_tile<GATEUP, 5>(t, smem, L, row_weight, act_out, contrib_out, cap); break;
+    case 6: gemm_tile<GATEUP, 6>(t, smem, L, row_weight, act_out, contrib_out, cap); break;
+    case 7: gemm_tile<GATEUP, 7>(t, smem, L, row_weight, act_out, contrib_out, cap); break;
+    default: gemm_tile<GATEUP, 8>(t, smem, L, row_weight, act_out, contrib_out, cap); break;
   }
 }
 
@@ -981,6 +1007,7 @@ struct LayerCall {
   int stride = 0;               // int32 words between top-k rows (0: k)
   bool routed_f32 = false;      // RunLayer output: f32 routed sum, no shared expert
   hipEvent_t ev[5] = {nullptr, nullptr, nullptr, nullptr, nullptr};
+  GemmCapture cap{nullptr, nullptr};  // optional f32 intermediates
 };
 
 static int record(hipEvent_t e, hipStream_t st) {
@@ -1004,7 +1031,7 @@ static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint1
     const int nt = d.I / 128;
     hipLaunchKernelGGL((grouped_gemm_kernel<true>), dim3(mtiles * nt), dim3(kGemmThreads), 0, st,
                        L, x, w.tiles, w.tile_count, w.token_map, w.row_weight, d.A, nt, w.act,
-                       w.contrib);
+                       w.contrib, call.cap);
   }
   rc = launch_check("grouped gate/up GEMM");
   if (rc != AIMA_OK) return rc;
@@ -1013,7 +1040,7 @@ static int prefill_layer(const aima_moe_layer& L, const uint16_t* x, const uint1
     const int nt = d.H / 256;
     hipLaunchKernelGGL((grouped_gemm_kernel<false>), dim3(mtiles * nt), dim3(kGemmThreads), 0, st,
                        L, w.act, w.tiles, w.tile_count, w.token_map, w.row_weight, d.A, nt, w.act,
-                       w.contrib);
+                       w.contrib, call.cap);
   }
   rc = launch_check("grouped down GEMM");
   if (rc != AIMA_OK) return rc;
@@ -1164,6 +1191,9 @@ extern "C" int aima_moe_grouped_prefill_ex(const aima_moe_layer* layer, const vo
   call.stride = (int)(stride_bytes / 4);
   call.routed_f32 = routed;
   for (int i = 0; i < 5; ++i) call.ev[i] = static_cast<hipEvent_t>(opt.stage_events[i]);
+  AIMA_REQUIRE(aligned(opt.swiglu_f32, 16) && aligned(opt.contributions_f32, 16),
+               "moe_grouped_prefill_ex: the f32 capture buffers must be 16-byte aligned");
+  call.cap = GemmCapture{opt.swiglu_f32, opt.contributions_f32};
   const uint16_t* x16 = static_cast<const uint16_t*>(x);
   if (opt.input_f32) {
     const int64_t n8 = tokens * layer->hidden / 8;
@@ -1177,6 +1207,47 @@ extern "C" int aima_moe_grouped_prefill_ex(const aima_moe_layer* layer, const vo
                        CombineNext{}, call);
 }
 
+// MOE3GemmFusedCompressed's operation: router logits in, the selection of
+// select_router_topk per token (the router top-k kernel, ids and weights into
+// the caller's buffers), then the grouped layer of aima_moe_grouped_prefill_ex
+// on those dense routes.
+extern "C" int aima_moe_grouped_prefill_logits(const aima_moe_layer* layer, const void* x,
+                                               const uint16_t* residual, int64_t tokens,
+                                               const float* routing_logits, int32_t k,
+                                               float min_weight_sum, int32_t* ids_out,
+                                               float* weights_out, void* out,
+                                               const aima_prefill_options* options,
+                                               void* workspace, size_t workspace_bytes,
+                                               void* stream) {
+  AIMA_REQUIRE(layer && x && routing_logits && ids_out && weights_out && out,
+               "moe_grouped_prefill_logits: null pointer");
+  aima_prefill_options opt{};
+  if (options) opt = *options;
+  AIMA_REQUIRE(opt.topk_stride == 0 || opt.topk_stride == (int64_t)k * 4,
+               "moe_grouped_prefill_logits: the routes are dense (topk_stride 0)");
+  AIMA_REQUIRE(tokens > 0 && tokens <= (1 << 24),
+               "moe_grouped_prefill_logits: tokens must be in [1, 2^24]");
+  // everything the layer call checks, before the selection is launched
+  int rc = check_layer_prefill(layer, k, false, opt.output_mode != AIMA_PREFILL_ROUTED_F32);
+  if (rc != AIMA_OK) return rc;
+  AIMA_REQUIRE(min_weight_sum > 0.f,
+               "moe_grouped_prefill_logits: minimum weight sum must be positive");
+  const PrefillDims d = prefill_dims(layer, tokens, k);
+  if (!workspace || workspace_bytes < prefill_ws_layout(d, WsMode::kLayer, nullptr, nullptr)) {
+    return fail(AIMA_E_WORKSPACE, "moe_grouped_prefill_logits: workspace missing or too small");
+  }
+  const hipStream_t st = (hipStream_t)stream;
+  hipEvent_t first = static_cast<hipEvent_t>(opt.stage_events[0]);
+  if ((rc = record(first, st)) != AIMA_OK) return rc;
+  opt.stage_events[0] = nullptr;  // event 0 marks the start of the selection
+  rc = aima_router_topk(routing_logits, tokens, layer->experts, k, min_weight_sum, ids_out,
+                        weights_out, stream);
+  if (rc != AIMA_OK) return rc;
+  opt.topk_stride = 0;
+  return aima_moe_grouped_prefill_ex(layer, x, residual, tokens, ids_out, weights_out, k, out,
+                                     &opt, workspace, workspace_bytes, stream);
+}
+
 extern "C" int aima_moe_prefill_workspace_views(const aima_moe_layer* layer, int64_t tokens,
                                                 int32_t k, void* workspace,
                                                 aima_prefill_views* views) {
@@ -1188,7 +1259,7 @@ extern "C" int aima_moe_prefill_workspace_views(const aima_moe_layer* layer, int
   views->token_map = w.token_map;
   views->inverse_map = w.inverse_map;
   views->compact_weights = w.row_weight;
-  views->weighted_swiglu = w.act;
+  views->swiglu = w.act;
   views->contributions = w.contrib;
   views->tiles = w.tiles;
   views->tile_count = w.tile_count;

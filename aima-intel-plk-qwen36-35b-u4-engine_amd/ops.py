@@ -538,16 +538,19 @@ def grouped_moe_prefill(layer: MoeLayerWeights, x: torch.Tensor, ids: torch.Tens
 def grouped_moe_prefill_routed(layer: MoeLayerWeights, hidden_states: torch.Tensor,
                                topk: torch.Tensor, router_weights: torch.Tensor,
                                topk_stride: Optional[int] = None, expert_used_count: int = 8,
-                               ws: Optional[Workspace] = None, stage_events=None) -> torch.Tensor:
+                               ws: Optional[Workspace] = None, stage_events=None,
+                               capture_f32: Optional[dict] = None) -> torch.Tensor:
     """GroupedS8U4PrefillRuntime::RunLayer's operation: the f32 routed sum
-    out[t] = sum_r w[t][r] * down_r(swiglu(gate_up_r x_t)) (no shared expert,
-    no residual).
+    out[t] = sum_r f16(w[t][r] * down_r(f16(swiglu(gate_up_r x_t)))) (no
+    shared expert, no residual).
 
     hidden_states: float32 or float16 [T, H]; topk: int32 ids with token t's
     ``expert_used_count`` ids at byte offset t * topk_stride (a 2-D [T, >= k]
     tensor uses its row stride; a flat int32 or uint8 buffer needs
     ``topk_stride``); router_weights: float32 [T * k] (or [T, k]).
     stage_events: optional five torch.cuda.Event recorded around the stages.
+    capture_f32: a dict that receives "swiglu_f32" [T*k, I] and
+    "contributions_f32" [T*k, H] (schedule order, before f16 rounding).
     """
     _require_cuda(hidden_states, topk, router_weights)
     if hidden_states.dtype not in (torch.float32, torch.float16) or hidden_states.dim() != 2 \
@@ -595,16 +598,69 @@ def grouped_moe_prefill_routed(layer: MoeLayerWeights, hidden_states: torch.Tens
             if e is not None and not e.cuda_event:
                 e.record(torch.cuda.current_stream())  # torch creates its events lazily
             opt.stage_events[i] = e.cuda_event if e is not None else None
+    if capture_f32 is not None:
+        capture_f32["swiglu_f32"] = torch.empty((T * k, layer.inter), dtype=torch.float32,
+                                                device=x.device)
+        capture_f32["contributions_f32"] = torch.empty((T * k, layer.hidden),
+                                                       dtype=torch.float32, device=x.device)
+        opt.swiglu_f32 = capture_f32["swiglu_f32"].data_ptr()
+        opt.contributions_f32 = capture_f32["contributions_f32"].data_ptr()
     call("aima_moe_grouped_prefill_ex", C.byref(lc), x.data_ptr(), None, T, topk.data_ptr(),
          rw.data_ptr(), k, out.data_ptr(), C.byref(opt), buf.data_ptr(), buf.numel(), _stream())
     return out
 
 
+def moe_3gemm_fused_compressed(hidden_states: torch.Tensor, routing_logits: torch.Tensor,
+                               layer: MoeLayerWeights, expert_used_count: int = 8,
+                               min_weight_sum: float = MIN_WEIGHT_SUM,
+                               include_shared: bool = False,
+                               residual: Optional[torch.Tensor] = None,
+                               ws: Optional[Workspace] = None):
+    """MOE3GemmFusedCompressed(hidden, routing_logits, gate_*, up_*, down_*)
+    (engine/openvino/iq36-fixed-fc-moe-router-compat.patch:31-56): the
+    routes are selected on the device from the f32 logits [T, E] (the
+    select_router_topk rule) and the grouped layer runs on them.  Returns
+    (out, ids int32 [T, k], weights float32 [T, k]); out is the f32 routed
+    sum [T, H] (the op's output), or with ``include_shared`` the f16 block
+    output with the sigmoid-gated shared expert (+ ``residual``).
+    ``layer`` holds the gate and up projections either concatenated or
+    split (``layer.to_split()``, the op's separate gate_* / up_* inputs)."""
+    _require_cuda(hidden_states, routing_logits, residual)
+    x = hidden_states.contiguous()
+    if x.dim() != 2 or x.shape[1] != layer.hidden or x.dtype not in (torch.float16,
+                                                                       torch.float32):
+        raise ValueError("hidden_states must be float16 or float32 [tokens, hidden]")
+    T = x.shape[0]
+    k = int(expert_used_count)
+    if routing_logits.dtype != torch.float32 or tuple(routing_logits.shape) != (T, layer.experts) \
+            or not routing_logits.is_contiguous():
+        raise ValueError("routing_logits must be contiguous float32 [tokens, experts]")
+    if include_shared and x.dtype != torch.float16:
+        raise ValueError("the full block output takes float16 hidden states")
+    if residual is not None and not include_shared:
+        raise ValueError("a residual needs include_shared")
+    lc = layer.c()
+    ws = _ws(ws, x.device)
+    buf = ws.get(size_query("aima_moe_prefill_workspace_size", C.byref(lc), T, k))
+    ids = torch.empty((T, k), dtype=torch.int32, device=x.device)
+    w = torch.empty((T, k), dtype=torch.float32, device=x.device)
+    opt = _lib.PrefillOptionsC()
+    opt.output_mode = _lib.AIMA_PREFILL_FULL_F16 if include_shared else _lib.AIMA_PREFILL_ROUTED_F32
+    opt.input_f32 = 1 if x.dtype == torch.float32 else 0
+    out = torch.empty((T, layer.hidden), dtype=torch.float16 if include_shared else torch.float32,
+                      device=x.device)
+    call("aima_moe_grouped_prefill_logits", C.byref(lc), x.data_ptr(), _ptr(residual), T,
+         routing_logits.data_ptr(), k, float(min_weight_sum), ids.data_ptr(), w.data_ptr(),
+         out.data_ptr(), C.byref(opt), buf.data_ptr(), buf.numel(), _stream())
+    return out, ids, w
+
+
 def prefill_workspace_views(layer: MoeLayerWeights, tokens: int, k: int, ws: Workspace,
                             with_shared: bool = True) -> dict:
     """Tensor views of the intermediates the last prefill call left in ``ws``
-    (schedule, router-weighted SwiGLU rows and down contributions, in
-    schedule order; aliases of the workspace, valid until its next use)."""
+    (schedule, unweighted f16 SwiGLU rows and router-weighted f16 down
+    contributions, in schedule order; aliases of the workspace, valid until
+    its next use)."""
     if ws.buf is None:
         raise ValueError("workspace was never used")
     lc = layer.c()
@@ -624,8 +680,8 @@ def prefill_workspace_views(layer: MoeLayerWeights, tokens: int, k: int, ws: Wor
             "token_map": view(v.token_map, A, torch.int32),
             "inverse_map": view(v.inverse_map, A, torch.int32),
             "compact_weights": view(v.compact_weights, A, torch.float32),
-            "weighted_swiglu": view(v.weighted_swiglu, rows * layer.inter,
-                                    torch.float16).reshape(rows, layer.inter),
+            "swiglu": view(v.swiglu, rows * layer.inter,
+                           torch.float16).reshape(rows, layer.inter),
             "contributions": view(v.contributions, rows * layer.hidden,
                                   torch.float16).reshape(rows, layer.hidden),
             "tile_count": view(v.tile_count, 1, torch.int32)}

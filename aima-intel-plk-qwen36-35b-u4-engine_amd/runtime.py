@@ -68,9 +68,12 @@ class GroupedU4PrefillTiming:
 @dataclass
 class GroupedU4PrefillRun:
     output: torch.Tensor
-    # intermediates (capture_intermediates), in schedule order:
-    grouped_weighted_swiglu_f16: Optional[torch.Tensor] = None  # w_r * silu(g) * u, [rows][I]
-    grouped_contributions_f16: Optional[torch.Tensor] = None    # w_r * down, [rows][H]
+    # intermediates (capture_intermediates), in schedule order, as the
+    # reference's run record (grouped_s8_u4_prefill_runtime.hpp:101-107):
+    grouped_swiglu_f16: Optional[torch.Tensor] = None          # silu(g) * u, [rows][I]
+    grouped_swiglu_f32: Optional[torch.Tensor] = None          # same, before f16 rounding
+    grouped_contributions_f16: Optional[torch.Tensor] = None   # w_r * down, [rows][H]
+    grouped_contributions_f32: Optional[torch.Tensor] = None   # same, before f16 rounding
     inverse_map: Optional[torch.Tensor] = None
     token_map: Optional[torch.Tensor] = None
     offsets: Optional[torch.Tensor] = None
@@ -147,7 +150,7 @@ class GroupedU4PrefillRuntime:
         # events: router start, then the prefill call's own five
         stage_events = [torch.cuda.Event(enable_timing=True) for _ in range(len(STAGES) + 1)]
 
-        def execute(events=None):
+        def execute(events=None, capture=None):
             if inp.include_shared:
                 return ops.grouped_moe_prefill(layer, x, inp.topk,
                                                inp.router_weights.reshape(T, k),
@@ -161,18 +164,22 @@ class GroupedU4PrefillRuntime:
             return ops.grouped_moe_prefill_routed(layer, x, topk, rw, topk_stride=st,
                                                   expert_used_count=k, ws=self._ws,
                                                   stage_events=None if events is None
-                                                  else events[1:])
+                                                  else events[1:], capture_f32=capture)
 
         for _ in range(inp.warmup):
             execute()
         stream = torch.cuda.current_stream()
         samples, stages = [], []
         out = None
-        for _ in range(inp.repeat):
+        # the last timed repeat also writes the f32 intermediates (as the
+        # reference's kernels write theirs next to the f16 ones)
+        capture = {} if inp.capture_intermediates and not inp.include_shared else None
+        for i in range(inp.repeat):
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
             start.record(stream)
-            out = execute(None if inp.include_shared else stage_events)
+            out = execute(None if inp.include_shared else stage_events,
+                          capture if i == inp.repeat - 1 else None)
             end.record(stream)
             end.synchronize()
             samples.append(start.elapsed_time(end) * 1000.0)
@@ -195,8 +202,11 @@ class GroupedU4PrefillRuntime:
             run.inverse_map = v["inverse_map"].clone()
             run.token_map = v["token_map"].clone()
             run.offsets = v["offsets"].clone()
-            run.grouped_weighted_swiglu_f16 = v["weighted_swiglu"].clone()
+            run.grouped_swiglu_f16 = v["swiglu"].clone()
             run.grouped_contributions_f16 = v["contributions"].clone()
+            if capture:
+                run.grouped_swiglu_f32 = capture["swiglu_f32"]
+                run.grouped_contributions_f32 = capture["contributions_f32"]
             run.gateup_work_tile_count = int(v["tile_count"].item()) * (layer.inter // 128)
             run.active_experts = int((counts > 0).sum().item())
             run.max_group_size = int(counts.max().item())

@@ -181,10 +181,12 @@ int aima_router_gemm_workspace_size(int64_t tokens, int64_t hidden,
 /* Router for a batch of tokens (the grouped prefill's native router,
  * grouped_s8_u4_prefill_runtime.cpp:1085-1101; its weights are f32,
  * kRouterWeightBytes = experts x hidden x 4 at :35): logits[T][E] =
- * hidden_states[T][H] . router_weight[E][H]^T in f32 (rocBLAS sgemm on
- * `stream`), then the selection of aima_router_topk per token: ids[T][k],
- * weights[T][k] (normalized).  hidden_states is f32 (input_f32 = 1) or f16
- * (0: widened to f32 in the workspace first).  experts <= 1024, k <= 16. */
+ * hidden_states[T][H] . router_weight[E][H]^T in f32 (f32 matrix-core
+ * GEMM on `stream`), then the selection of aima_router_topk per token:
+ * ids[T][k], weights[T][k] (normalized).  hidden_states is f32
+ * (input_f32 = 1) or f16 (0: widened to f32 in the workspace first).
+ * hidden % 16 == 0, hidden_states and router_weight 16-byte aligned,
+ * experts <= 1024, k <= 16. */
 int aima_router_gemm_topk(const void* hidden_states, int32_t input_f32,
                           int64_t tokens, int64_t hidden,
                           const float* router_weight, int32_t experts, int32_t k,
@@ -387,6 +389,13 @@ typedef struct aima_prefill_options {
   void* stage_events[5];  /* optional hipEvent_t, recorded on `stream` before the
                              schedule and after the schedule, the gate/up GEMM,
                              the down GEMM and the combine (NULL entries skipped) */
+  float* swiglu_f32;      /* optional f32 [rows][inter], 16-byte aligned: the SwiGLU
+                             rows before their f16 rounding (RunLayer's
+                             grouped_swiglu_f32); rows in schedule order, T*k routed
+                             rows (+ T shared rows in the full mode) */
+  float* contributions_f32; /* optional f32 [rows][hidden], 16-byte aligned: w_row *
+                             down(row) before its f16 rounding (RunLayer's
+                             grouped_contributions_f32; shared rows unweighted) */
 } aima_prefill_options;
 
 /* Grouped MoE FFN over T tokens with GroupedS8U4PrefillRuntime::RunLayer's
@@ -401,15 +410,39 @@ typedef struct aima_prefill_options {
  *              grouped_s8_u4_f16_contribution_moe.cl:831-845); no shared
  *              expert (its tensors may be NULL) and no residual;
  *            AIMA_PREFILL_FULL_F16: f16 [T][hidden] as aima_moe_grouped_prefill.
+ * The arithmetic follows the reference's grouped kernels
+ * (grouped_s8_u4_f16_contribution_moe.cl:627-683): each row's SwiGLU is
+ * rounded to f16 unweighted, the down projection consumes it, and the router
+ * weight multiplies the down output before its f16 rounding.
  * Out-of-range or duplicated ids set the workspace error word (RunLayer
  * throws).  Workspace as aima_moe_prefill_workspace_size; the schedule, the
- * weighted SwiGLU rows and the contributions of the call stay in it (see
- * aima_moe_prefill_workspace_views). */
+ * f16 SwiGLU rows and the contributions of the call stay in it (see
+ * aima_moe_prefill_workspace_views); f32 copies go to the option buffers. */
 int aima_moe_grouped_prefill_ex(const aima_moe_layer* layer, const void* x,
                                 const uint16_t* residual, int64_t tokens,
                                 const int32_t* topk, const float* weights, int32_t k,
                                 void* out, const aima_prefill_options* options,
                                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* The grouped prefill fed router logits, as OpenVINO's fused MoE op
+ * MOE3GemmFusedCompressed(hidden, routing_logits, gate_*, up_*, down_*)
+ * (engine/openvino/iq36-fixed-fc-moe-router-compat.patch:31-56,183-193):
+ * routing_logits f32 [T][experts] -> per token the selection of
+ * aima_router_topk (select_router_topk: f64 softmax, k largest, lower id on
+ * ties, renormalized by max(sum, min_weight_sum)) written to ids_out [T][k]
+ * and weights_out [T][k], then aima_moe_grouped_prefill_ex on those dense
+ * routes (options as there; topk_stride must be 0; stage event 0 is
+ * recorded before the selection).  Workspace as
+ * aima_moe_prefill_workspace_size.  One launch more than the layer (the
+ * selection); the routes pass through ids_out / weights_out. */
+int aima_moe_grouped_prefill_logits(const aima_moe_layer* layer, const void* x,
+                                    const uint16_t* residual, int64_t tokens,
+                                    const float* routing_logits, int32_t k,
+                                    float min_weight_sum, int32_t* ids_out,
+                                    float* weights_out, void* out,
+                                    const aima_prefill_options* options,
+                                    void* workspace, size_t workspace_bytes,
+                                    void* stream);
 
 /* Device pointers into a prefill workspace: the intermediates the last
  * aima_moe_grouped_prefill(_ex) call on it left there (RunLayer's
@@ -422,8 +455,11 @@ typedef struct aima_prefill_views {
   int32_t* token_map;        /* [T*k] source token of each routed row */
   int32_t* inverse_map;      /* [T*k] row of (token, rank) */
   float* compact_weights;    /* [T*k] router weight of each routed row */
-  uint16_t* weighted_swiglu; /* f16 [T*k + T][inter]: w_row * silu(gate) * up */
-  uint16_t* contributions;   /* f16 [T*k + T][hidden]: down of the row above */
+  uint16_t* swiglu;          /* f16 [T*k + T][inter]: silu(gate) * up, unweighted
+                                (RunLayer's grouped_swiglu_f16) */
+  uint16_t* contributions;   /* f16 [T*k + T][hidden]: w_row * down of the row
+                                above (shared rows unweighted; RunLayer's
+                                grouped_contributions_f16) */
   int32_t* tiles;            /* [tile_count][4] expert, first row, rows, 0 */
   int32_t* tile_count;       /* one int */
 } aima_prefill_views;

@@ -258,7 +258,7 @@ def test_prefill_workspace_views(pkg):
     L.call("aima_moe_prefill_workspace_views", C.byref(lc), T, k, C.c_void_p(base), C.byref(v))
     A = T * k
     spans = [(v.offsets, 256 * 4), (v.tiles, 16), (v.token_map, A * 4), (v.inverse_map, A * 4),
-             (v.compact_weights, A * 4), (v.weighted_swiglu, (A + T) * 512 * 2),
+             (v.compact_weights, A * 4), (v.swiglu, (A + T) * 512 * 2),
              (v.contributions, (A + T) * 2048 * 2)]
     end = base
     for ptr, n in spans:
@@ -300,3 +300,15 @@ def test_split_layout_round_trip(pkg):
     assert sp.expert_bytes() == layer.expert_bytes()
     c = sp.c()
     assert c.up.qweight == sp.up.qweight.data_ptr() and layer.c().up.qweight is None
+
+
+def test_router_gemm_validation(pkg):
+    """The batched router rejects shapes its GEMM does not implement before
+    any launch (hidden % 16, 16-byte alignment)."""
+    L = pkg._lib
+    lib = L.lib()
+    p = C.c_void_p(1 << 20)
+    odd = C.c_void_p((1 << 20) + 4)
+    args = lambda x, H: (x, 1, 64, H, p, 256, 8, C.c_float(6.1e-5), p, p, p, None, 0, None)
+    assert lib.aima_router_gemm_topk(*args(p, 2040)) == L.AIMA_E_INVALID
+    assert lib.aima_router_gemm_topk(*args(odd, 2048)) == L.AIMA_E_INVALID

@@ -147,13 +147,27 @@ def test_run_layer_intermediates_and_stages(pkg, dev, layer_c2):
     for r in range(k):
         acc = acc + contrib[inv[:, r]]
     assert torch.equal(acc, run.output)
-    # weighted SwiGLU rows against the oracle's SwiGLU times the router weight
+    # the run record's intermediates, as the reference's
+    # (grouped_s8_u4_prefill_runtime.hpp:101-107): SwiGLU rows unweighted in
+    # f16 and f32, contributions w_r * down in f16 and f32; each f16 row is
+    # the f32 one rounded to nearest even, bit for bit
+    A = T * k
+    sw16, sw32 = run.grouped_swiglu_f16, run.grouped_swiglu_f32
+    c16, c32 = run.grouped_contributions_f16[:A], run.grouped_contributions_f32
+    assert sw32.shape == (A, 512) and c32.shape == (A, 2048)
+    assert torch.equal(sw16[:A], sw32.half())
+    assert torch.equal(c16, c32.half())
     for t in (0, T // 2, T - 1):
         d = oracle.moe_ffn_token_detail(mw, f16_to_f32(x[t]), None, ids[t].cpu().numpy(),
                                         w[t].cpu().numpy())
-        sw = d["selected_swiglu"].reshape(k, 512) * w[t].cpu().numpy()[:, None]
-        got = run.grouped_weighted_swiglu_f16[inv[t]].float().cpu().numpy()
-        assert_parity(got, sw, what=f"weighted swiglu token {t}")
+        wt = w[t].cpu().numpy()[:, None]
+        assert_parity(sw32[inv[t]].cpu().numpy(), d["selected_swiglu"].reshape(k, 512),
+                      what=f"swiglu f32 token {t}")
+        assert_parity(c32[inv[t]].cpu().numpy(), d["selected_down"].reshape(k, 2048) * wt,
+                      what=f"contributions f32 token {t}")
+    # capturing changes no arithmetic: a plain run gives the same output
+    again = rt.RunLayer(h, pkg.GroupedU4PrefillInput(x, ids, w.reshape(-1), repeat=1))
+    assert torch.equal(again.output, run.output)
     ref = oracle.moe_routed_tokens(mw, f16_to_f32(x), ids.cpu().numpy(), w.cpu().numpy(),
                                    threads=THREADS)
     assert_parity(run.output.cpu().numpy(), ref, what="runtime routed")
@@ -212,3 +226,43 @@ def test_split_decode_plan_matches(pkg, dev):
     assert torch.equal(a, b)
     pa.close()
     pb.close()
+
+
+@pytest.mark.parametrize("include_shared", [False, True])
+def test_moe_3gemm_fused_compressed_logits(pkg, dev, layer_c2, include_shared):
+    """MOE3GemmFusedCompressed's contract (aima_moe_grouped_prefill_logits):
+    router logits in, with the Zipf skew of config 2 and a run of tied
+    logits.  The device's routes are the oracle's select_router_topk on
+    those logits (ids exact, weights at 1e-6), the output equals the
+    ids-fed entry point on the same routes bit for bit, and sampled tokens
+    match the oracle at the 2e-3 bar.  Split gate / up tensors, as the op
+    takes them."""
+    layer, mw = layer_c2
+    split = layer.to_split()
+    T, E, k = 2048, 256, 8
+    x = pkg.synth.activations(T, 2048, 130, dev)
+    logits = pkg.synth.router_logits(T, E, 131, dev, zipf_s=1.1)
+    logits[5, 40:52] = logits[5].max() + 1.0  # 12 equal top logits: ids decide
+    res = pkg.synth.activations(T, 2048, 132, dev) if include_shared else None
+    out, ids, w = pkg.moe_3gemm_fused_compressed(x, logits, split, k,
+                                                 include_shared=include_shared, residual=res)
+    torch.cuda.synchronize()
+    ref_ids, ref_w = oracle.router_topk_tokens(logits.cpu().numpy(), k)
+    assert np.array_equal(ids.cpu().numpy(), ref_ids)
+    assert ids[5].cpu().tolist() == list(range(40, 48))
+    assert_parity(w.cpu().numpy(), ref_w, tol=1e-6, what="fused-op router weights")
+    if include_shared:
+        fed = pkg.grouped_moe_prefill(layer, x, ids, w, residual=res)
+    else:
+        fed = pkg.grouped_moe_prefill_routed(layer, x, ids, w.reshape(-1))
+    torch.cuda.synchronize()
+    assert torch.equal(out, fed)
+    sel = np.array([0, 5, 1000, T - 1])
+    xs = f16_to_f32(x)[sel]
+    if include_shared:
+        ref = oracle.moe_ffn_tokens(mw, xs, ref_ids[sel], ref_w[sel],
+                                    residual=f16_to_f32(res)[sel], threads=THREADS)
+        assert_parity(f16_to_f32(out)[sel], ref, what="fused-op full output")
+    else:
+        ref = oracle.moe_routed_tokens(mw, xs, ref_ids[sel], ref_w[sel], threads=THREADS)
+        assert_parity(out.cpu().numpy()[sel], ref, what="fused-op routed output")

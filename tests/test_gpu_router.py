@@ -21,9 +21,13 @@ def _router(E, H, seed, dev):
     return (torch.randn((E, H), generator=g, device=dev) * 0.05).contiguous()
 
 
-@pytest.mark.parametrize("T,E,k", [(300, 256, 8), (1, 256, 8), (2048, 256, 8), (77, 16, 4)])
-def test_router_gemm_topk(pkg, dev, T, E, k):
-    H = 2048
+@pytest.mark.parametrize("T,E,k,H", [(300, 256, 8, 2048), (1, 256, 8, 2048),
+                                     (2048, 256, 8, 2048), (77, 16, 4, 2048),
+                                     (33, 100, 8, 528)])
+def test_router_gemm_topk(pkg, dev, T, E, k, H):
+    """Tiles of 64 tokens x 64 experts: partial tiles in both dimensions
+    (T = 1, 33, 77, 300; E = 16, 100) and a hidden size whose K halves are
+    not a multiple of the 64-wide steps (528)."""
     x = pkg.synth.activations(T, H, T + E, dev).float()
     W = _router(E, H, T + 1, dev)
     ids, w, logits = pkg.router_gemm_topk(x, W, k)
