@@ -47,6 +47,7 @@
 
 #include <math.h>
 
+#include <cstdlib>
 #include <string>
 #include <vector>
 
@@ -58,6 +59,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / 64;
+constexpr int kStreamWaves = 1;                          // the streaming wave (ring instance)
+constexpr int kRingThreads = kThreads + 64 * kStreamWaves;
 constexpr int kH = 2048;                                 // hidden (specialization)
 constexpr int kI = 512;                                  // expert intermediate (specialization)
 constexpr int kXcds = 8;
@@ -233,6 +236,20 @@ struct SharedState {
   int reroute;                         // routed plan: the layer's route changed
   int32_t rank[kMaxK + 1];             // routed plan: ranks 0..k by logit
 };
+
+// One slot of the weight ring (ring instance): everything the 8 compute
+// waves of a block read for one layer, in the per-lane order they read it.
+// Written by the streaming wave one layer ahead (two slots: layer L reads
+// slot L & 1 while layer L + 1's rows fill the other).
+struct RingSlot {
+  u32x4 a[kRowsA][64];                 // gate/up rows: block row ri, lane l's 32 nibbles
+  u32x4 b[kWaves][2][64];              // routed down rows of wave w, units 0 and 1
+  u32x4 bs[kWaves][16];                // shared down slice of wave w (16 lanes' chunks)
+  uint32_t as[kRowsA][8];              // gate/up scale words (16 f16 scales per row)
+  uint32_t az[kRowsA][2];              // gate/up zero-point words (16 nibbles per row)
+  uint32_t bg[kWaves][40];             // down scale / zero-point words (gather_b order)
+};
+static_assert(sizeof(RingSlot) % 16 == 0, "ring slots stay 16-byte aligned");
 
 // Router top-k for one layer (one wave): f64 softmax over the logits,
 // (probability desc, id asc) selection, renormalization by max(sum, min).
@@ -633,9 +650,19 @@ __device__ uint64_t* g_trace = nullptr;
 // exchanges them XCD-locally, and one wave of every block selects the top-k;
 // only then are the layer's routed gate/up and down rows loaded.  Otherwise
 // the routes of all layers come from the launch's logits or ids.
-template <bool G128, bool ROUTED>
-__global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistArgs a) {
+// RING (with G128, logits-fed only): a ninth wave streams every layer's
+// rows into the LDS weight ring one layer ahead with ordinary global loads,
+// at most one batch (18 row loads) in flight; the compute waves then issue
+// no weight loads at all, so their dot products never stall on a full
+// memory queue.  The streaming wave passes exactly the barriers the compute
+// waves pass (see stream_rows below).
+template <bool G128, bool ROUTED, bool RING = false>
+__global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_persistent_kernel(
+    PersistArgs a) {
+  static_assert(!RING || (G128 && !ROUTED), "the ring serves the logits-fed 128-group plan");
   __shared__ SharedState S;
+  __shared__ __attribute__((aligned(16))) uint8_t ring_mem[RING ? 2 * sizeof(RingSlot) : 16];
+  RingSlot* const ring = reinterpret_cast<RingSlot*>(ring_mem);
   const int lane = threadIdx.x & 63;
   // wave-uniform values in scalar registers, so per-row branches and buffer
   // offsets below are scalar and never merge divergent loads
@@ -710,13 +737,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     uint32_t* dst = reinterpret_cast<uint32_t*>(S.table);
     const int words = a.n_layers * (int)(sizeof(PlanLayer) / 4);
     const int first = ROUTED ? 0 : 64;  // wave 0 routes in the logits-fed plan
-    for (int i = (int)threadIdx.x - first; i >= 0 && i < words; i += kThreads - first) {
+    for (int i = (int)threadIdx.x - first; i >= 0 && i < words && wave < kWaves;
+         i += kThreads - first) {
       dst[i] = src[i];
     }
   }
   __syncthreads();
   // lane l of wave w reads slot l & 7 of layer L0 + w + 8 (l >> 3)
-  for (int L0 = 0; !ROUTED && L0 < a.n_layers; L0 += 8 * kWaves) {
+  for (int L0 = 0; !ROUTED && wave < kWaves && L0 < a.n_layers; L0 += 8 * kWaves) {
     const int L = L0 + wave + kWaves * (lane >> 3);
     const int s = lane & 7;
     const bool mine = L < a.n_layers && s < k;
@@ -1123,7 +1151,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
 #pragma unroll
     for (int i = 0; i < kMaxRowsA; ++i) {
       const int ri = ((wave + 4) & 7) + kWaves * i;
-      if (!ROUTED) {
+      if (!ROUTED && !RING) {
         if (L + 1 < a.n_layers) prefetch_a1(S.table[L + 1], slot_expert(L + 1), i);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -1139,12 +1167,205 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     }
   };
 
+  // ---- the streaming wave (ring instance) -------------------------------------
+  // Layer M's rows go to ring slot M & 1 in four batches (t = 0, 1: gate/up
+  // rows 18 t .. 18 t + 17; t = 2: the gate/up scale and zero-point words and
+  // the routed down rows of unit 0 of the 8 compute waves; t = 3: the routed
+  // down rows of unit 1, the shared down slices and the down scale and
+  // zero-point words).  The addresses are prefetch_a1's, gather_a's,
+  // prefetch_b's and gather_b's for every compute wave in turn.  Batch t of
+  // layer L + 1 is issued after barrier #(t + 1) of layer L and written to
+  // LDS after the next barrier, so at most one batch (18 KB) is in flight and
+  // everything of layer L + 1 is in its slot by barrier #1 of layer L + 1
+  // (the compute waves read gate/up rows after #2, down rows after #4;
+  // layer 0: the compute waves fill slot 0 themselves).  Slot (L + 1) & 1 was
+  // last read in phase B of layer L - 1, which ends before barrier #1 of
+  // layer L; the first write into it follows barrier #2 of layer L.  The wave
+  // passes the same barriers as the compute waves -- the two of the prologue
+  // above, then #1 .. #4 of every layer -- and returns where they return
+  // (S.abort is only written before a barrier that precedes its check).
+  auto stream_rows = [&]() {
+    u32x4 buf[kPairs];      // row loads in flight (one batch)
+    uint32_t g2[6], g3[5];  // scale / zero-point words of batches 2 and 3
+    constexpr int kGateWords = kRowsA * 10;  // 8 scale + 2 zero-point words per row
+    // (lane-derived offsets from a fresh opaque lane index per call: hoisted
+    // out of the layer loop they would stay live across it and spill)
+    auto issue = [&](int M, int t, int at) {
+      const int ln = opaque_v(threadIdx.x & 63);
+      const PlanLayer& T = S.table[M];
+      const uint32_t e = slot_expert(M);
+      const uint64_t eq = (uint64_t)e * T.estride_q, es = (uint64_t)e * T.estride_s,
+                     ez = (uint64_t)e * T.estride_z;
+      if (t < 2) {
+        const AIMA_GLOBAL uint8_t *rq0 = uptr(T.gq0) + eq, *rq1 = uptr(T.gq1) + eq;
+        const AIMA_GLOBAL uint8_t *hq0 = uptr(T.sq0), *hq1 = uptr(T.sq1);
+#pragma unroll
+        for (int q = 0; q < kPairs; ++q) {
+          const int ri = kPairs * t + q;
+          const bool h = (ri & 1) != 0;
+          const int p = j * kPairs + (ri >> 1);
+          const bool routed = p < kI;
+          const int unit = routed ? p : x * kSlice + (p - kI);
+          buf[at + q] = ld_w(routed ? (h ? rq1 : rq0) : (h ? hq1 : hq0),
+                             (uint32_t)unit * (kH / 2) + ln * 16);
+        }
+        return;
+      }
+      const AIMA_GLOBAL uint8_t* dw = uptr(T.dq) + (size_t)e * ((uint32_t)kH * (kI / 2));
+      if (t == 2) {
+        const AIMA_GLOBAL uint8_t *rs0 = uptr(T.gs0) + es, *rs1 = uptr(T.gs1) + es;
+        const AIMA_GLOBAL uint8_t *rz0 = uptr(T.gz0) + ez, *rz1 = uptr(T.gz1) + ez;
+        const AIMA_GLOBAL uint8_t *hs0 = uptr(T.ss0), *hs1 = uptr(T.ss1);
+        const AIMA_GLOBAL uint8_t *hz0 = uptr(T.sz0), *hz1 = uptr(T.sz1);
+#pragma unroll
+        for (int g = 0; g < 6; ++g) {
+          const int q = min(64 * g + ln, kGateWords - 1);
+          const int ri = q / 10, w10 = q % 10;
+          const bool h = (ri & 1) != 0;
+          const int p = j * kPairs + (ri >> 1);
+          const bool routed = p < kI;
+          const int unit = routed ? p : x * kSlice + (p - kI);
+          const bool is_s = w10 < 8;
+          const AIMA_GLOBAL uint8_t* base =
+              is_s ? (routed ? (h ? rs1 : rs0) : (h ? hs1 : hs0))
+                   : (routed ? (h ? rz1 : rz0) : (h ? hz1 : hz0));
+          const uint32_t off = is_s ? (uint32_t)unit * 32 + 4 * w10
+                                    : (uint32_t)unit * 8 + 4 * (w10 - 8);
+          g2[g] = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
+        }
+#pragma unroll
+        for (int wv = 0; wv < kWaves; ++wv) {
+          const int row = j * kRowsB + wv * kWaveRowsB + (ln >> 4);
+          buf[at + wv] = ld_w(dw, (uint32_t)row * (kI / 2) + (ln & 15) * 16);
+        }
+        return;
+      }
+#pragma unroll
+      for (int wv = 0; wv < kWaves; ++wv) {
+        const int row = j * kRowsB + wv * kWaveRowsB + 4 + (ln >> 4);
+        buf[at + wv] = ld_w(dw, (uint32_t)row * (kI / 2) + (ln & 15) * 16);
+      }
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int wv = 4 * g + (ln >> 4);
+        const int row = j * kRowsB + wv * kWaveRowsB + ((ln & 15) >> 1);
+        buf[at + kWaves + g] =
+            ld_w(uptr(T.sdq), (uint32_t)x * (kH * 32) + row * 32 + (ln & 1) * 16);
+      }
+      const uint32_t sbytes = (uint32_t)kH * 4 * 2;
+      const uint32_t zbytes = (uint32_t)kH * 4 / 2;
+      const AIMA_GLOBAL uint8_t* rs = uptr(T.ds) + (size_t)e * sbytes;
+      const AIMA_GLOBAL uint8_t* rz = uptr(T.dz) + (size_t)e * zbytes;
+      const AIMA_GLOBAL uint8_t* hs = uptr(T.sds);
+      const AIMA_GLOBAL uint8_t* hz = uptr(T.sdz);
+#pragma unroll
+      for (int g = 0; g < 5; ++g) {
+        const int q = 64 * g + ln;  // 320 words: 40 per wave
+        const int wv = q / 40, qq = q % 40;
+        const uint32_t h0 = (uint32_t)(j * kRowsB + wv * kWaveRowsB);
+        const AIMA_GLOBAL uint8_t* base = qq < 16 ? rs : qq < 20 ? rz : qq < 36 ? hs : hz;
+        const uint32_t off = qq < 16   ? h0 * 8 + 4 * qq
+                             : qq < 20 ? h0 * 2 + 4 * (qq - 16)
+                             : qq < 36 ? h0 * 8 + 4 * (qq - 20)
+                                       : h0 * 2 + 4 * (qq - 36);
+        g3[g] = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
+      }
+    };
+    auto write = [&](int M, int t, int at) {
+      const int ln = opaque_v(threadIdx.x & 63);
+      RingSlot& R = ring[M & 1];
+      if (t < 2) {
+#pragma unroll
+        for (int q = 0; q < kPairs; ++q) R.a[kPairs * t + q][ln] = buf[at + q];
+        return;
+      }
+      if (t == 2) {
+#pragma unroll
+        for (int g = 0; g < 6; ++g) {
+          const int q = 64 * g + ln;
+          if (q < kGateWords) {
+            const int ri = q / 10, w10 = q % 10;
+            if (w10 < 8) {
+              R.as[ri][w10] = g2[g];
+            } else {
+              R.az[ri][w10 - 8] = g2[g];
+            }
+          }
+        }
+#pragma unroll
+        for (int wv = 0; wv < kWaves; ++wv) R.b[wv][0][ln] = buf[at + wv];
+        return;
+      }
+#pragma unroll
+      for (int wv = 0; wv < kWaves; ++wv) R.b[wv][1][ln] = buf[at + wv];
+#pragma unroll
+      for (int g = 0; g < 2; ++g) R.bs[4 * g + (ln >> 4)][ln & 15] = buf[at + kWaves + g];
+#pragma unroll
+      for (int g = 0; g < 5; ++g) {
+        const int q = 64 * g + ln;
+        R.bg[q / 40][q % 40] = g3[g];
+      }
+    };
+    for (int L = 0; L < a.n_layers; ++L) {
+      const int M = L + 1;
+      const bool more = M < a.n_layers;
+      __syncthreads();  // #1
+      if (S.abort) return;
+      if (L > 0) write(L, 3, 0);
+      if (more) issue(M, 0, 0);
+      __syncthreads();  // #2
+      if (more) {
+        write(M, 0, 0);
+        issue(M, 1, 0);
+      }
+      __syncthreads();  // #3
+      if (more) {
+        write(M, 1, 0);
+        issue(M, 2, 0);
+      }
+      __syncthreads();  // #4
+      if (S.abort) return;
+      if (more) {
+        write(M, 2, 0);
+        issue(M, 3, 0);
+      }
+    }
+  };
+  if constexpr (RING) {
+    if (wave == kWaves) {
+      stream_rows();
+      return;
+    }
+  }
   load_vec(0);
   if (ROUTED) {
     prefetch_router(0);
   } else {
     prefetch_a(S.table[0], slot_expert(0));
     prefetch_b(S.table[0], slot_expert(0));
+  }
+  if (RING) {
+    // layer 0's rows: every compute wave writes what it loaded into slot 0,
+    // in the streaming wave's layout (row slots past the block's 36 rows and
+    // the duplicate lanes of the shared slice and the gathers write nothing)
+    RingSlot& R = ring[0];
+    const int ln = opaque_v(threadIdx.x & 63);
+#pragma unroll
+    for (int i = 0; i < kMaxRowsA; ++i) {
+      const int ri = ((wave + 4) & 7) + kWaves * i;
+      if (ri < kRowsA) R.a[ri][ln] = wa_n[i];
+    }
+    if (ln < 40) {
+      const int ri = ((wave + 4) & 7) + kWaves * (ln >> 3);
+      if (ri < kRowsA) R.as[ri][ln & 7] = gsa_n;
+    } else if (ln < 50) {
+      const int ri = ((wave + 4) & 7) + kWaves * ((ln - 40) >> 1);
+      if (ri < kRowsA) R.az[ri][(ln - 40) & 1] = gsa_n;
+    }
+    R.b[wave][0][ln] = wb_n[0];
+    R.b[wave][1][ln] = wb_n[1];
+    if (ln < 16) R.bs[wave][ln] = wb_n[2];
+    if (ln < 40) R.bg[wave][ln] = gsb_n;
   }
   AIMA_TRACE(40, 1, 0);  // prologue done
 
@@ -1200,7 +1421,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       finish();
       return;
     }
-    if (!ROUTED) {
+    if (RING) {
+      // the rows come from the ring after barrier #2 and #4
+    } else if (!ROUTED) {
       rotate_a();
       rotate_b();
     } else {
@@ -1256,7 +1479,18 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
     AIMA_TRACE(L, 2, 0);
     if (!ROUTED && L + 1 < a.n_layers) {
       load_vec(L + 1);
-      prefetch_b(S.table[L + 1], slot_expert(L + 1));
+      if (!RING) prefetch_b(S.table[L + 1], slot_expert(L + 1));
+    }
+    if (RING) {
+      // this layer's gate/up rows and their scale / zero-point words
+      const RingSlot& R = ring[L & 1];
+#pragma unroll
+      for (int i = 0; i < kMaxRowsA; ++i) {
+        const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
+        wa[i] = R.a[ri][ln];
+        sa[i] = R.as[ri][ln >> 3];
+        za[i] = R.az[ri][ln >> 5];
+      }
     }
     {
       XChunk xc;
@@ -1434,6 +1668,23 @@ __global__ __launch_bounds__(kThreads, 1) void decode_persistent_kernel(PersistA
       rotate_b();
       AIMA_TRACE(L, 20, 0);  // down rows in registers (wave 0)
     }
+    if (RING) {
+      // this layer's down rows and their scale / zero-point words (the
+      // lanes of rotate_b's picks)
+      const RingSlot& R = ring[L & 1];
+      wb[0] = R.b[wave][0][ln];
+      wb[1] = R.b[wave][1][ln];
+      wb[2] = R.bs[wave][ln & 15];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int r = 4 * u + (ln >> 4);
+        sb[u] = R.bg[wave][2 * r + ((ln & 15) >> 3)];
+        zb[u] = R.bg[wave][16 + (r >> 1)];
+      }
+      const int r8 = (ln & 15) >> 1;
+      sb[2] = R.bg[wave][20 + 2 * r8 + (x >> 2)];
+      zb[2] = R.bg[wave][36 + (r8 >> 1)];
+    }
     // ================= phase B_L =================
     {
       const int h0 = j * kRowsB + wave * kWaveRowsB;
@@ -1545,6 +1796,7 @@ using namespace aima;
 
 struct aima_moe_decode_plan {
   int device = 0;
+  bool ring = false;  // logits-fed 128-group runs take the weight-ring instance
   int n_layers = 0;
   int k = 0;
   int experts = 0;
@@ -1666,6 +1918,13 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
     AIMA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, kThreads, 0));
     per_cu = std::min(per_cu, n);
   }
+  {
+    int n = 0;
+    AIMA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &n, reinterpret_cast<const void*>(decode_persistent_kernel<true, false, true>),
+        kRingThreads, 0));
+    per_cu = std::min(per_cu, n);
+  }
   const int blocks = kBlocks;  // one block per CU: 8 XCDs x 32 CUs
   (void)coop;
   if (cus != kBlocks || per_cu < 1) {
@@ -1695,6 +1954,9 @@ extern "C" int aima_moe_decode_plan_create(const aima_moe_layer* layers, int32_t
   const size_t o_sdq = take(kSliceBytes * n_layers);
   aima_moe_decode_plan* p = new aima_moe_decode_plan();
   p->device = dev;
+  // AIMA_DECODE_RING=0 keeps the register-prefetch instance (A/B runs)
+  const char* ring_env = std::getenv("AIMA_DECODE_RING");
+  p->ring = !(ring_env && ring_env[0] == '0');
   p->n_layers = n_layers;
   p->k = k;
   p->experts = layers[0].experts;
@@ -1761,17 +2023,19 @@ int plan_launch(aima_moe_decode_plan* plan, PersistArgs& a, bool routed, void* s
   a.err = plan->err;
   void* args[] = {&a};
   const bool g128 = plan->group_log2 == 7;
+  const bool ring = !routed && g128 && plan->ring;
   const void* kern =
-      routed ? (g128 ? reinterpret_cast<const void*>(decode_persistent_kernel<true, true>)
-                     : reinterpret_cast<const void*>(decode_persistent_kernel<false, true>))
-             : (g128 ? reinterpret_cast<const void*>(decode_persistent_kernel<true, false>)
-                     : reinterpret_cast<const void*>(decode_persistent_kernel<false, false>));
+      ring ? reinterpret_cast<const void*>(decode_persistent_kernel<true, false, true>)
+      : routed ? (g128 ? reinterpret_cast<const void*>(decode_persistent_kernel<true, true>)
+                       : reinterpret_cast<const void*>(decode_persistent_kernel<false, true>))
+               : (g128 ? reinterpret_cast<const void*>(decode_persistent_kernel<true, false>)
+                       : reinterpret_cast<const void*>(decode_persistent_kernel<false, false>));
   // A regular launch: with one block per CU on 256 CUs every block becomes
   // resident (work of other streams only delays placement).  A cooperative
   // launch would guarantee it against concurrent persistent launches too,
   // but measured 18 us slower per launch (the gap between launches).
-  AIMA_HIP(hipLaunchKernel(kern, dim3(plan->blocks), dim3(kThreads), args, 0,
-                           (hipStream_t)stream));
+  AIMA_HIP(hipLaunchKernel(kern, dim3(plan->blocks), dim3(ring ? kRingThreads : kThreads), args,
+                           0, (hipStream_t)stream));
   return AIMA_OK;
 }
 

@@ -236,6 +236,28 @@ def test_stack_prefill_fused_combine_three_layers(pkg, dev):
 # resident persistent decode (one launch for all layers)
 # ---------------------------------------------------------------------------
 
+def test_decode_plan_ring_matches_register_prefetch(pkg, dev, monkeypatch):
+    """The weight-ring instance (the default for 128-wide groups: a streaming
+    wave fills an LDS ring one layer ahead) and the register-prefetch
+    instance (AIMA_DECODE_RING=0) run the same arithmetic on the same rows:
+    bit-identical outputs, repeated runs, k = 8 and k = 3."""
+    layers = make_stack(pkg, dev, 3, 2048, 512, 16, seed=990)
+    monkeypatch.setenv("AIMA_DECODE_RING", "0")
+    plain = {k: pkg.DecodePlan(layers, k=k) for k in (8, 3)}
+    monkeypatch.delenv("AIMA_DECODE_RING")
+    ring = {k: pkg.DecodePlan(layers, k=k) for k in (8, 3)}
+    for rep in range(3):
+        x = pkg.synth.activations(1, 2048, 991 + rep, dev)[0].contiguous()
+        logits = torch.stack([pkg.synth.router_logits(1, 16, 995 + 10 * rep + l, dev)[0]
+                              for l in range(3)])
+        for k in (8, 3):
+            a = plain[k].run(x, router_logits=logits)
+            b = ring[k].run(x, router_logits=logits)
+            torch.cuda.synchronize()
+            assert plain[k].error_bits() == 0 and ring[k].error_bits() == 0
+            assert torch.equal(a, b), (rep, k)
+
+
 def test_decode_plan_small_stack(pkg, dev):
     """3 layers of the real width (16 experts): persistent kernel vs oracle,
     routing from logits and from explicit ids/weights; repeated runs (the
@@ -393,6 +415,16 @@ def test_config4a_decode_plan_40_layers(pkg, dev, stack40):
         one.close()
         r = nxt
     assert torch.equal(chained, out), "40-layer plan differs from 40 chained 1-layer plans"
+    # the register-prefetch instance gives the same 40-layer result
+    os.environ["AIMA_DECODE_RING"] = "0"
+    try:
+        plain = pkg.DecodePlan(stack40, k=8)
+    finally:
+        del os.environ["AIMA_DECODE_RING"]
+    again = plain.run(x[0], router_logits=logits)
+    torch.cuda.synchronize()
+    assert plain.error_bits() == 0 and torch.equal(again, out)
+    plain.close()
     chains = stack_chains(mws, norms, f16_bits(x), rids, w_np, EPS, oracle.MODEL_DECODE_PLAN,
                           THREADS)
     assert np.array_equal(chains["ref"], r)
