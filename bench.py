@@ -554,7 +554,7 @@ def matvec_bench(torch, ops, synth, layers, layers_c, dev, ids_buf, w_buf):
     out["config3_lm_head_N248320"] = {"us": round(us, 2), "gbs": round(b3 / us / 1e3, 1),
                                       "hbm_frac": round(b3 / us / 1e3 / HBM_PEAK_GBS, 4),
                                       "bytes": b3}
-    # the same LM head with its top-8 (logits kept, one selection launch):
+    # the same LM head with its top-8 (logits kept; one launch at K = 2048):
     # back-to-back calls through the C ABI with preallocated outputs (the
     # Python wrapper's allocations and size query would outlast the GPU
     # work, and a graph replay adds its own launch overhead on this system)

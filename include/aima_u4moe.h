@@ -253,9 +253,14 @@ int aima_topk_f32(const float* values, int64_t n, int32_t k, int32_t* ids,
 
 /* U4 LM head with top-k: logits = f32 U4 matvec of x (as aima_u4_matvec,
  * kept in the caller's logits buffer of n floats), then aima_topk_f32 over
- * them (same workspace rules).  Replaces the reference's
+ * them (same results and workspace rules).  Replaces the reference's
  * q4s_group128_lm_head_topk8_f32 (engine/gpu/opencl/q4x8_matvec.cl:973-1021:
- * logits out plus per-block partial top-8 ids and values) with its merge. */
+ * logits out plus per-block partial top-8 ids and values) with its merge.
+ * At K = 2048 with a workspace (and ceil(n / 2048) * topk <= 1024) it is one
+ * launch: the matvec's blocks also store each logit in the workspace as a
+ * 64-bit word {bits, tag of (bits, launch number)}, and the selection's
+ * blocks, dispatched after them, read their chunk once every word carries
+ * this launch's tag.  AIMA_LM_HEAD_FUSED=0 selects the two launches. */
 int aima_u4_lm_head_topk(const uint16_t* x, const uint8_t* qweight,
                          const uint16_t* scale, const uint8_t* zp, int64_t n,
                          int64_t k, int32_t group, int32_t topk, float* logits,

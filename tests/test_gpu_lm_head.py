@@ -54,6 +54,63 @@ def test_topk_distinct_and_infinite(pkg, dev):
     assert np.array_equal(ids.cpu().numpy(), ref_i) and np.array_equal(vals.cpu().numpy(), ref_v)
 
 
+def _crowded(n, k, dev, seed):
+    """Values whose best keys crowd into few 16-lane rows of each block: the
+    positions a block's rows k // 2 .. 15 read (p % 256 >= 16 * (k // 2),
+    for chunks that start at multiples of 256) hold -1 - |noise|, the rest
+    10 + noise.  The threshold (the k-th best row best) then admits
+    thousands of survivors, the selection's per-wave fallback."""
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    p = torch.arange(n, device=dev)
+    noise = torch.randn(n, generator=g, device=dev)
+    low = (p % 256) >= 16 * max(k // 2, 1)
+    return torch.where(low, -1.0 - noise.abs(), 10.0 + noise)
+
+
+@pytest.mark.parametrize("n", [4096, 8192, 65536, 300000])
+@pytest.mark.parametrize("k", [2, 8, 16])
+def test_topk_crowded_rows(pkg, dev, n, k):
+    v = _crowded(n, k, dev, n + k)
+    ids, vals = pkg.topk_f32(v, k)
+    torch.cuda.synchronize()
+    ref_i, ref_v = oracle.lm_head_topk(v.cpu().numpy(), k)
+    assert np.array_equal(ids.cpu().numpy(), ref_i)
+    assert np.array_equal(vals.cpu().numpy(), ref_v)
+
+
+@pytest.mark.parametrize("k", [8, 16])
+def test_topk_signed_zeros(pkg, dev, k):
+    """+0 and -0 are equal values (the lower index first) and each pick's
+    value keeps its own sign bit."""
+    n = 70001
+    g = torch.Generator(device=dev)
+    g.manual_seed(k)
+    v = -1.0 - torch.rand(n, generator=g, device=dev)
+    zp = torch.randperm(n, generator=g, device=dev)[:40]
+    sign = torch.randint(0, 2, (40,), generator=g, device=dev).float() * 2 - 1
+    v[zp] = 0.0 * sign  # -0.0 where sign is -1
+    ids, vals = pkg.topk_f32(v, k)
+    torch.cuda.synchronize()
+    ref_i, _ = oracle.lm_head_topk(v.cpu().numpy(), k)
+    assert np.array_equal(ids.cpu().numpy(), ref_i)
+    assert ids.cpu().tolist() == sorted(zp.cpu().tolist())[:k]
+    want = v[ids.long()].cpu().numpy().view(np.int32)
+    assert np.array_equal(vals.cpu().numpy().view(np.int32), want)
+    assert (want == np.int32(-2**31)).any() and (want == 0).any()
+
+
+def test_lm_head_topk_crowded_rows(pkg, dev):
+    """The one-launch head (chunks of 2,048 at n = 65,536) with logits whose
+    best crowd into few rows of every selection block."""
+    n, K = 65536, 2048
+    for k in (8, 16):
+        scales = _crowded(n, k, "cpu", 7 + k)
+        w = _structured_head(pkg, dev, n, K, scales)
+        x = torch.full((K,), 0.25, dtype=torch.float16, device=dev)
+        _check_head(pkg, dev, w, x, k)
+
+
 @pytest.mark.parametrize("k", [1, 8, 16])
 def test_lm_head_topk_config3(pkg, dev, k):
     """K=2048, N=248320: logits are the matvec's bit for bit, the selection is
@@ -128,11 +185,12 @@ def test_lm_head_topk_ordered_and_tied(pkg, dev, order, k):
         assert ids.cpu().tolist() == list(range(k))
 
 
-@pytest.mark.parametrize("K", [128, 512, 8192])
+@pytest.mark.parametrize("K", [128, 512, 2048, 8192])
 @pytest.mark.parametrize("n,k", [(5, 5), (700, 16), (33333, 8)])
 def test_lm_head_topk_shapes(pkg, dev, K, n, k):
     """Every block geometry (512 rows per block at K = 128 down to 16 at
-    K = 8192), partial last blocks and n = k."""
+    K = 8192), partial last blocks and n = k; at K = 2048 the one-launch
+    head with one selection block (n <= 4096) and with several."""
     gen = pkg.synth.generator(K + n + k, dev)
     w = pkg.synth.u4_weight(1, n, K, 128, gen, dev)
     x = pkg.synth.activations(1, K, K + n, dev)[0]
@@ -186,6 +244,21 @@ def test_lm_head_topk_state_reused_between_calls(pkg, dev):
         torch.cuda.synchronize()
         ref_i, _ = oracle.lm_head_topk(v.cpu().numpy(), 8)
         assert np.array_equal(ids.cpu().numpy(), ref_i)
+    assert ws.error_bits() == 0
+
+
+@pytest.mark.parametrize("n", [700, 4096, 4097])
+def test_lm_head_topk_small_vocab_reused(pkg, dev, n):
+    """The one-launch head with one selection block advances the launch
+    counter itself (no merge does): calls on one workspace with new inputs
+    each select from their own logits, never the tagged logits an earlier
+    call left in place (n = 4097 takes two selection blocks and the merge)."""
+    ws = pkg.Workspace(dev)
+    gen = pkg.synth.generator(n, dev)
+    w = pkg.synth.u4_weight(1, n, 2048, 128, gen, dev)
+    for seed in range(4):
+        x = pkg.synth.activations(1, 2048, 50 + seed, dev)[0]
+        _check_head(pkg, dev, w, x, 8, ws=ws)
     assert ws.error_bits() == 0
 
 
