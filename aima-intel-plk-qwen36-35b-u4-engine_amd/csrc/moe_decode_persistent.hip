@@ -966,17 +966,17 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
     }
     if (g128) gather_b(Ly, e);
   };
-  // All gate/up and down rows of layer L in one burst (routed plan): the
-  // table fields are read first and each row's base chosen by selects, so the
-  // loads leave back to back (the loaders above read the table per row,
-  // which the prefetch interleaved with the dot products can afford; a burst
-  // that starts when the route is known cannot).  Same rows, lanes and
-  // clamping as prefetch_a, gather_a, prefetch_b and gather_b, but the
-  // gate/up rows go straight into the working registers, the gathering load
-  // first: each dot product then waits for its own row only (take_gather_a
-  // hands the scale and zero-point words out once the gather has landed).
-  // The down rows go to the prefetch registers (rotate_b at barrier #4).
-  auto issue_rows = [&](int L) {
+  // All gate/up rows of layer L in one burst (routed plan): the table fields
+  // are read first and each row's base chosen by selects, so the loads leave
+  // back to back (the loaders above read the table per row, which the
+  // prefetch interleaved with the dot products can afford; a burst that
+  // starts when the route is known cannot).  Same rows, lanes and clamping
+  // as prefetch_a and gather_a, but the rows go straight into the working
+  // registers, the gathering load first: each dot product then waits for its
+  // own row only (take_gather_a hands the scale and zero-point words out once
+  // the gather has landed).  The layer's down rows follow with prefetch_b
+  // once the wave's gate/up dot products are done (see the routed layer).
+  auto issue_rows_a = [&](int L) {
     const int ln = opaque_v(threadIdx.x & 63);
     const PlanLayer& T = S.table[L];
     const uint32_t e = slot_expert(L);
@@ -988,10 +988,6 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
     const AIMA_GLOBAL uint8_t *hq0 = uptr(T.sq0), *hq1 = uptr(T.sq1);
     const AIMA_GLOBAL uint8_t *hs0 = uptr(T.ss0), *hs1 = uptr(T.ss1);
     const AIMA_GLOBAL uint8_t *hz0 = uptr(T.sz0), *hz1 = uptr(T.sz1);
-    const AIMA_GLOBAL uint8_t* dw = uptr(T.dq) + (size_t)e * ((uint32_t)kH * (kI / 2));
-    const AIMA_GLOBAL uint8_t* dsc = uptr(T.ds) + (size_t)e * ((uint32_t)kH * gB * 2);
-    const AIMA_GLOBAL uint8_t* dzp = uptr(T.dz) + (size_t)e * ((uint32_t)kH * gB / 2);
-    const AIMA_GLOBAL uint8_t *sw = uptr(T.sdq), *ssc = uptr(T.sds), *szp = uptr(T.sdz);
     if (g128) {
       const int q = min(ln, 49);
       const bool is_s = q < 40;
@@ -1023,38 +1019,6 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         sa[i] = ld_u32(routed ? (h ? rs1 : rs0) : (h ? hs1 : hs0), (gi * 2) & ~3);
         za[i] = ld_u32(routed ? (h ? rz1 : rz0) : (h ? hz1 : hz0), (gi >> 1) & ~3);
       }
-    }
-    // down rows
-    const int h0 = j * kRowsB + wave * kWaveRowsB;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int row = h0 + 4 * u + (ln >> 4);
-      const int cl = ln & 15;
-      wb_n[u] = ld_w(dw, (uint32_t)row * (kI / 2) + cl * 16);
-      if (!g128) {
-        const int gi = row * gB + ((cl * 32) >> glog2);
-        sb_n[u] = ld_u32(dsc, (gi * 2) & ~3);
-        zb_n[u] = ld_u32(dzp, (gi >> 1) & ~3);
-      }
-    }
-    {
-      const int row = h0 + ((ln & 15) >> 1);
-      const int ch = 2 * x + (ln & 1);
-      wb_n[2] = ld_w(sw, (uint32_t)x * (kH * 32) + row * 32 + (ln & 1) * 16);
-      if (!g128) {
-        const int gi = row * gB + ((ch * 32) >> glog2);
-        sb_n[2] = ld_u32(ssc, (gi * 2) & ~3);
-        zb_n[2] = ld_u32(szp, (gi >> 1) & ~3);
-      }
-    }
-    if (g128) {
-      const int q = min(ln, 39);
-      const AIMA_GLOBAL uint8_t* base = q < 16 ? dsc : q < 20 ? dzp : q < 36 ? ssc : szp;
-      const uint32_t off = q < 16   ? (uint32_t)h0 * 8 + 4 * q
-                           : q < 20 ? (uint32_t)h0 * 2 + 4 * (q - 16)
-                           : q < 36 ? (uint32_t)h0 * 8 + 4 * (q - 20)
-                                    : (uint32_t)h0 * 2 + 4 * (q - 36);
-      gsb_n = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
     }
   };
   // this wave's 256 norm-weight floats and gate-vector halves: lane l holds
@@ -1545,10 +1509,10 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
           finish();
           return;
         }
-        // every wave issues the layer's gate/up and down rows from that
-        // ranking; wave 1 then checks it while the loads are in flight (a
-        // changed route is loaded again after barrier #3)
-        issue_rows(L);
+        // every wave issues the layer's gate/up rows from that ranking; wave
+        // 1 then checks it while the loads are in flight (a changed route is
+        // loaded again after barrier #3)
+        issue_rows_a(L);
         AIMA_TRACE(L, 14, 128);  // loads issued (wave 2)
         AIMA_TRACE(L, 18, 64);   // loads issued (wave 1)
         if (wave == 1) {
@@ -1576,6 +1540,11 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         AIMA_TRACE(L, 19, 256);  // gate/up scales in registers (wave 4)
       }
       dots_a(xc, L);
+      // routed plan: the layer's down rows once the wave's gate/up rows are
+      // consumed.  Issued with the gate/up burst they shared each CU's
+      // memory queue with it and delayed the last gate/up row; here they
+      // land during the SwiGLU, the activation exchange and its staging.
+      if (ROUTED) prefetch_b(S.table[L], slot_expert(L));
     }
     if (wave == 0) {
       // shared-expert gate sigma = sigmoid(gate_vec . x), per block
@@ -1592,11 +1561,12 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
     if (ROUTED && S.reroute) {
       // the probabilities did not confirm the ranking (ties or near ties):
       // the confirmed route's rows, and the dot products again
-      issue_rows(L);
+      issue_rows_a(L);
       take_gather_a();
       XChunk xc;
       get_chunk(S.xa_p, S.xa_bias, S.xa_xsum, ln, xc);
       dots_a(xc, L);
+      prefetch_b(S.table[L], slot_expert(L));
       __syncthreads();  // #3r: row sums of the confirmed route
     }
     AIMA_TRACE(L, 4, 0);

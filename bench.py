@@ -6,7 +6,8 @@ Headline workload (BASELINE.json metric "MoE-FFN decode us/token + HBM GB/s
 config 4 (40 x 256 routed experts + 40 shared experts resident, hidden 2048,
 expert intermediate 512, group-128 U4, ~17 GB), one batch-1 decode step per
 "step": router top-8 from seeded logits for all 40 layers, then RMSNorm ->
-MoE FFN -> residual through every layer.  ``value`` is us per decode token.
+MoE FFN -> residual through every layer; consecutive steps take four seeded
+routings in turn.  ``value`` is us per decode token.
 
 The same line carries
 * ``roofline``: the dominant kernel, the persistent decode kernel (one launch
@@ -42,6 +43,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
 H, I, E, K_TOP, GROUP, LAYERS = 2048, 512, 256, 8, 128, 40
 EPS = 1e-6
+ROUTE_SETS = 4  # routings the decode steps take in turn
 
 
 def log(msg):
@@ -321,7 +323,13 @@ def main():
 
     # ------------------------------------------------------------------ decode
     x = synth.activations(1, H, 41, dev)[0].contiguous()
-    logits = torch.stack([synth.router_logits(1, E, 1041 + l, dev)[0] for l in range(LAYERS)])
+    # ROUTE_SETS routings (per-layer logits), taken in turn by consecutive
+    # steps of the persistent plan, so that no step re-reads the experts the
+    # step before it read (the union over the sets, ~2 GB, is far past the
+    # 256 MB last-level cache)
+    logit_sets = [torch.stack([synth.router_logits(1, E, 1041 + 97 * s + l, dev)[0]
+                               for l in range(LAYERS)]) for s in range(ROUTE_SETS)]
+    logits = logit_sets[0]
     ws = ops.Workspace(dev)
     out = torch.empty(H, dtype=torch.float16, device=dev)
     ids_buf = torch.empty((LAYERS, K_TOP), dtype=torch.int32, device=dev)
@@ -355,13 +363,23 @@ def main():
     rplan.close()
     del rplan, routers
     plan = ops.DecodePlan(layers, k=K_TOP)
+    step_no = [0]
+
+    def decode_step_set(sidx):
+        plan.run(x, router_logits=logit_sets[sidx], epsilon=EPS, out=out)
 
     def decode_step():
-        plan.run(x, router_logits=logits, epsilon=EPS, out=out)
+        decode_step_set(step_no[0] % ROUTE_SETS)
+        step_no[0] += 1
 
     eager_us = timed(torch, decode_step, args.steps, warmup=args.warmup)
     log(f"decode persistent eager: {eager_us:.1f} us/token")
-    replay = graphed(torch, decode_step)
+    replays = [graphed(torch, lambda s=s: decode_step_set(s)) for s in range(ROUTE_SETS)]
+
+    def replay():
+        replays[step_no[0] % ROUTE_SETS]()
+        step_no[0] += 1
+
     graph_us = timed(torch, replay, args.steps, warmup=args.warmup)
     log(f"decode persistent graph: {graph_us:.1f} us/token")
     plan.check()
@@ -395,6 +413,7 @@ def main():
         "data": "synthetic (seeded U4 weights, f16 activations, f32 router logits)",
         "config": {"workload": "config4a: 40-layer MoE FFN decode step, batch 1, top-8/256 + "
                                "shared expert, hidden 2048, inter 512, U4 group 128",
+                   "routings": ROUTE_SETS,
                    "layers": LAYERS, "experts": E, "top_k": K_TOP, "hidden": H, "inter": I,
                    "group": GROUP, "parallelism": "single-gpu"},
         "decode": {"us_per_token": round(step_us, 2), "eager_us": round(eager_us, 2),
