@@ -247,6 +247,17 @@ def test_lm_head_topk_state_reused_between_calls(pkg, dev):
     assert ws.error_bits() == 0
 
 
+@pytest.mark.parametrize("group", [32, 64, 256])
+def test_lm_head_topk_one_launch_groups(pkg, dev, group):
+    """The one-launch head (K = 2048) with every other quantization group
+    size: logits bit-identical to the plain matvec, picks the oracle's."""
+    n = 70001
+    gen = pkg.synth.generator(group + 5, dev)
+    w = pkg.synth.u4_weight(1, n, 2048, group, gen, dev)
+    x = pkg.synth.activations(1, 2048, group + 6, dev)[0]
+    _check_head(pkg, dev, w, x, 8)
+
+
 @pytest.mark.parametrize("n", [700, 4096, 4097])
 def test_lm_head_topk_small_vocab_reused(pkg, dev, n):
     """The one-launch head with one selection block advances the launch
