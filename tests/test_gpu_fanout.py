@@ -60,9 +60,11 @@ def test_multi_output_rejects_bad_calls(pkg, dev):
                       (C.c_void_p * 1)(None), (C.c_int32 * 1)(0), None)
 
 
-@pytest.mark.parametrize("experts,k", [(256, 8), (128, 4), (1000, 16)])
-def test_router_fc_topk(pkg, dev, experts, k):
-    router = _weight(pkg, dev, experts, 2048, 128, seed=experts)
+@pytest.mark.parametrize("experts,k,group", [(256, 8, 128), (128, 4, 128), (1000, 16, 128),
+                                             (256, 8, 32), (200, 8, 256), (17, 16, 64)])
+def test_router_fc_topk(pkg, dev, experts, k, group):
+    """Every expert count up to 1024 and every group size."""
+    router = _weight(pkg, dev, experts, 2048, group, seed=experts + group)
     x = pkg.synth.activations(1, 2048, seed=experts + 1, device=dev)
     norm = 1.0 + 0.01 * torch.randn(2048, device=dev, generator=pkg.synth.generator(7, dev))
     h = pkg.apply_rms_norm(x, norm, 1e-6)[0]
