@@ -25,6 +25,7 @@ router does.
 from __future__ import annotations
 
 import statistics
+import time
 from dataclasses import dataclass, field
 from typing import Dict, List, Optional
 
@@ -58,11 +59,31 @@ class GroupedU4PrefillInput:
 
 @dataclass
 class GroupedU4PrefillTiming:
+    """RunLayer's timing record (grouped_s8_u4_prefill_runtime.hpp:86-98).
+
+    input_upload_us: host -> device copy of host hidden states (0 when they
+    are already on the device); schedule_prepare_us: host work on the
+    schedule's inputs before the run (moving host top-k rows and router
+    weights to the device, repacking strided rows; 0 for dense device inputs
+    and for the native router); device_schedule_us: the device schedule
+    (count, scan, scatter kernels), median over the timed repeats from the
+    stage events; schedule_upload_us equals it and schedule_setup_us is
+    prepare + upload, as in the reference's device-schedule path
+    (grouped_s8_u4_prefill_runtime.cpp:1165-1168).  The samples include the
+    device schedule (it runs inside every repeat), so complete_minimum_us is
+    minimum_us + schedule_prepare_us (the reference adds its setup to
+    samples that exclude it, :1428-1429)."""
     stage_us: List[float] = field(default_factory=lambda: [0.0] * len(STAGES))
     samples_us: List[float] = field(default_factory=list)
     minimum_us: float = 0.0
     median_us: float = 0.0
     mean_us: float = 0.0
+    input_upload_us: float = 0.0
+    schedule_prepare_us: float = 0.0
+    schedule_upload_us: float = 0.0
+    schedule_setup_us: float = 0.0
+    device_schedule_us: float = 0.0
+    complete_minimum_us: float = 0.0
 
 
 @dataclass
@@ -127,7 +148,23 @@ class GroupedU4PrefillRuntime:
         layer = self._layer(handle)
         if inp.warmup < 0 or inp.repeat <= 0:
             raise ValueError("grouped prefill warmup/repeat are invalid")
+        # host inputs are copied to the device first, as the reference's
+        # WriteBuffer calls (timed with the host clock, copies complete)
+        input_upload_us = schedule_prepare_us = 0.0
         x = inp.hidden_states
+        if x.device.type != "cuda":
+            t0 = time.perf_counter()
+            x = x.to(self.device).contiguous()
+            torch.cuda.synchronize(self.device)
+            input_upload_us = (time.perf_counter() - t0) * 1e6
+        topk_in, rw_in = inp.topk, inp.router_weights
+        if not inp.native_router and (topk_in.device.type != "cuda" or
+                                      rw_in.device.type != "cuda"):
+            t0 = time.perf_counter()
+            topk_in = topk_in.to(self.device)
+            rw_in = rw_in.to(self.device)
+            torch.cuda.synchronize(self.device)
+            schedule_prepare_us = (time.perf_counter() - t0) * 1e6
         if x.dim() != 2 or x.shape[1] != layer.hidden:
             raise ValueError("grouped prefill hidden-state count mismatch")
         T, k = x.shape[0], int(inp.expert_used_count)
@@ -138,11 +175,11 @@ class GroupedU4PrefillRuntime:
             if inp.include_shared:
                 raise ValueError("native_router runs return the routed sum")
             router = self._routers[handle]
-        elif inp.router_weights.numel() != T * k:
+        elif rw_in.numel() != T * k:
             raise ValueError("grouped prefill router weight count mismatch")
         stride = inp.topk_stride or None
         if inp.include_shared:
-            if inp.topk.dtype != torch.int32 or inp.topk.shape != (T, k) or stride:
+            if topk_in.dtype != torch.int32 or topk_in.shape != (T, k) or stride:
                 raise ValueError("include_shared takes dense int32 top-k [T, k]")
             if x.dtype != torch.float16:
                 raise ValueError("include_shared takes float16 hidden states")
@@ -152,10 +189,10 @@ class GroupedU4PrefillRuntime:
 
         def execute(events=None, capture=None):
             if inp.include_shared:
-                return ops.grouped_moe_prefill(layer, x, inp.topk,
-                                               inp.router_weights.reshape(T, k),
+                return ops.grouped_moe_prefill(layer, x, topk_in,
+                                               rw_in.reshape(T, k),
                                                residual=inp.residual, ws=self._ws)
-            topk, rw, st = inp.topk, inp.router_weights, stride
+            topk, rw, st = topk_in, rw_in, stride
             if events is not None:
                 events[0].record(torch.cuda.current_stream())
             if router is not None:
@@ -193,6 +230,12 @@ class GroupedU4PrefillRuntime:
                                         mean_us=statistics.fmean(samples))
         if stages:
             timing.stage_us = [statistics.median(s[i] for s in stages) for i in range(len(STAGES))]
+        timing.input_upload_us = input_upload_us
+        timing.schedule_prepare_us = schedule_prepare_us
+        timing.device_schedule_us = timing.stage_us[1]
+        timing.schedule_upload_us = timing.device_schedule_us
+        timing.schedule_setup_us = timing.schedule_prepare_us + timing.schedule_upload_us
+        timing.complete_minimum_us = timing.minimum_us + timing.schedule_prepare_us
         run = GroupedU4PrefillRun(output=out, timing=timing, native_router=router is not None)
         if inp.capture_intermediates:
             # the last repeat's schedule and intermediates, still in the workspace

@@ -168,6 +168,24 @@ def test_run_layer_intermediates_and_stages(pkg, dev, layer_c2):
     # capturing changes no arithmetic: a plain run gives the same output
     again = rt.RunLayer(h, pkg.GroupedU4PrefillInput(x, ids, w.reshape(-1), repeat=1))
     assert torch.equal(again.output, run.output)
+    # the reference's timing record (grouped_s8_u4_prefill_runtime.hpp:86-98):
+    # device inputs need no upload or host preparation; the device schedule
+    # is the schedule stage; setup and complete minimum follow from them
+    tm = run.timing
+    assert tm.input_upload_us == 0.0 and tm.schedule_prepare_us == 0.0
+    assert tm.device_schedule_us == tm.stage_us[1] > 0
+    assert tm.schedule_upload_us == tm.device_schedule_us
+    assert tm.schedule_setup_us == tm.schedule_prepare_us + tm.schedule_upload_us
+    assert tm.complete_minimum_us == tm.minimum_us + tm.schedule_prepare_us
+    # host inputs are uploaded first (hidden states: input_upload_us; top-k
+    # rows and router weights: schedule_prepare_us), with the same output
+    host = rt.RunLayer(h, pkg.GroupedU4PrefillInput(x.cpu(), ids.cpu(), w.reshape(-1).cpu(),
+                                                    repeat=2))
+    assert torch.equal(host.output, run.output)
+    th = host.timing
+    assert th.input_upload_us > 0 and th.schedule_prepare_us > 0
+    assert th.schedule_setup_us == th.schedule_prepare_us + th.schedule_upload_us
+    assert th.complete_minimum_us == th.minimum_us + th.schedule_prepare_us
     ref = oracle.moe_routed_tokens(mw, f16_to_f32(x), ids.cpu().numpy(), w.cpu().numpy(),
                                    threads=THREADS)
     assert_parity(run.output.cpu().numpy(), ref, what="runtime routed")
