@@ -212,6 +212,19 @@ __device__ __forceinline__ void poll4(const void* p, int stride, uint64_t (&v)[4
 __device__ __forceinline__ uint32_t pack_word(uint16_t v, uint32_t epoch) {
   return (uint32_t)v | (epoch << 16);
 }
+// A lane's part of one row's dot product (u4_chunk_dot), rounded as written:
+// the empty asm keeps the compiler from fusing the final product into the
+// first step of the row sum that follows, which it does or not depending on
+// the surrounding code.  Every instance of the kernel (weight ring, register
+// prefetch, routed) must produce the same sums bit for bit.
+__device__ __forceinline__ float lane_dot(const u32x4 w, const XChunk& c, uint32_t z, float s,
+                                          uint32_t magic) {
+  float t = __builtin_fmaf(-(float)z, c.xsum, u4_chunk_raw(w, c, magic) - c.bias);
+  t = t * s;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 __device__ __forceinline__ uint64_t pack_f32(float v, uint32_t epoch) {
   return (uint64_t)__builtin_bit_cast(uint32_t, v) | ((uint64_t)epoch << 32);
 }
@@ -245,9 +258,16 @@ struct RingSlot {
   u32x4 a[kRowsA][64];                 // gate/up rows: block row ri, lane l's 32 nibbles
   u32x4 b[kWaves][2][64];              // routed down rows of wave w, units 0 and 1
   u32x4 bs[kWaves][16];                // shared down slice of wave w (16 lanes' chunks)
-  uint32_t as[kRowsA][8];              // gate/up scale words (16 f16 scales per row)
-  uint32_t az[kRowsA][2];              // gate/up zero-point words (16 nibbles per row)
-  uint32_t bg[kWaves][40];             // down scale / zero-point words (gather_b order)
+  // Scale and zero-point words, each kind in the order it lies in memory, so
+  // that the streaming wave loads and stores them lane by lane:
+  // as[h * 144 + 8 pp + w]: word w (16 f16 scales) of the block's pair pp,
+  // gate (h = 0) or up (h = 1); az[h * 36 + 2 pp + w]: its zero-point words;
+  // bgs[128 s + 16 wv + q]: scale word q of wave wv's 8 down rows, routed
+  // (s = 0) or the shared slice (s = 1); bgz[32 s + 4 wv + q]: zero points.
+  uint32_t as[2 * kPairs * 8];
+  uint32_t az[2 * kPairs * 2];
+  uint32_t bgs[2 * kWaves * 16];
+  uint32_t bgz[2 * kWaves * 4];
 };
 static_assert(sizeof(RingSlot) % 16 == 0, "ring slots stay 16-byte aligned");
 
@@ -627,11 +647,14 @@ __device__ __forceinline__ void lds_xchunk(const uint32_t* src, int w0, XChunk& 
 // Diagnostics build only (never in the product library): phase timestamps of
 // every block, 100 MHz real-time clock, g_trace[(L * 256 + block) * 32 + slot];
 // row 40 (the prologue) keeps the block's hardware XCD id in slot 31.
+// The stamps are global (not flat) stores: a flat store also counts against
+// the LDS counter, so every later LDS wait would wait for the stamp to land.
 __device__ uint64_t* g_trace = nullptr;
-#define AIMA_TRACE(L, slot, T)                                              \
-  do {                                                                      \
-    if (trace && threadIdx.x == (T) && b < 256)                             \
-      trace[((L) * 256 + b) * 32 + (slot)] = __builtin_amdgcn_s_memrealtime(); \
+#define AIMA_TRACE(L, slot, T)                                                   \
+  do {                                                                           \
+    if (trace && threadIdx.x == (T) && b < 256)                                  \
+      ((AIMA_GLOBAL uint64_t*)trace)[((L) * 256 + b) * 32 + (slot)] =            \
+          __builtin_amdgcn_s_memrealtime();                                      \
   } while (0)
 #else
 #define AIMA_TRACE(L, slot, T) \
@@ -684,7 +707,12 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
 #endif
   AIMA_TRACE(40, 0, 0);  // kernel entry
 #ifdef AIMA_DECODE_TRACE
-  if (trace && threadIdx.x == 0 && b < 256) trace[(40 * 256 + b) * 32 + 31] = (uint64_t)x;
+  if (trace && threadIdx.x == 0 && b < 256)
+    ((AIMA_GLOBAL uint64_t*)trace)[(40 * 256 + b) * 32 + 31] = (uint64_t)x;
+  // each wave's SIMD (HW_REG_HW_ID bits 5:4) in slots 16 + wave
+  if (trace && (threadIdx.x & 63) == 0 && b < 256)
+    ((AIMA_GLOBAL uint64_t*)trace)[(40 * 256 + b) * 32 + 16 + wave] =
+        (uint64_t)__builtin_amdgcn_s_getreg((1 << 11) | (4 << 6) | 4);
 #endif
 
   if (threadIdx.x == 0) S.abort = 0;
@@ -1125,7 +1153,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         const int unit = p < kI ? p : x * kSlice + (p - kI);
         const int gi = unit * gA + ((ln * 32) >> glog2);
         const float dd =
-            segment_sum<64>(u4_chunk_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
+            segment_sum<64>(lane_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
         if ((threadIdx.x & 63) == 0 && ri < kRowsA) S.rowsum[ri] = dd;
       }
     }
@@ -1150,8 +1178,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
   // (S.abort is only written before a barrier that precedes its check).
   auto stream_rows = [&]() {
     u32x4 buf[kPairs];      // row loads in flight (one batch)
-    uint32_t g2[6], g3[5];  // scale / zero-point words of batches 2 and 3
-    constexpr int kGateWords = kRowsA * 10;  // 8 scale + 2 zero-point words per row
+    uint32_t g2[8], g3[5];  // scale / zero-point words of batches 2 and 3
     // (lane-derived offsets from a fresh opaque lane index per call: hoisted
     // out of the layer loop they would stay live across it and spill)
     auto issue = [&](int M, int t, int at) {
@@ -1177,26 +1204,29 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       }
       const AIMA_GLOBAL uint8_t* dw = uptr(T.dq) + (size_t)e * ((uint32_t)kH * (kI / 2));
       if (t == 2) {
-        const AIMA_GLOBAL uint8_t *rs0 = uptr(T.gs0) + es, *rs1 = uptr(T.gs1) + es;
-        const AIMA_GLOBAL uint8_t *rz0 = uptr(T.gz0) + ez, *rz1 = uptr(T.gz1) + ez;
-        const AIMA_GLOBAL uint8_t *hs0 = uptr(T.ss0), *hs1 = uptr(T.ss1);
-        const AIMA_GLOBAL uint8_t *hz0 = uptr(T.sz0), *hz1 = uptr(T.sz1);
+        // The block's pairs are consecutive units -- routed up to pair
+        // kI - 1, then shared-slice units -- so each kind of word is one
+        // run in memory (gate scales, up scales, gate zero points, up zero
+        // points): lane-linear loads, word u from the routed tensor while u
+        // is below the routed pairs' words, else from the shared one.
+        const int p0 = j * kPairs;            // the block's first pair
+        const int su = x * kSlice - kI + p0;  // shared unit of pair p0 (< 0: routed pairs first)
+        const int rp = kI - p0;               // routed pairs of the block (<= 0: none)
+        auto word = [&](const AIMA_GLOBAL uint8_t* r, const AIMA_GLOBAL uint8_t* h, int per,
+                        int u) {  // per: bytes per unit
+          const bool routed = u < rp * (per / 4);
+          const uint32_t off = (uint32_t)(4 * u + (routed ? p0 : su) * per);
+          return *reinterpret_cast<const AIMA_GLOBAL uint32_t*>((routed ? r : h) + off);
+        };
 #pragma unroll
-        for (int g = 0; g < 6; ++g) {
-          const int q = min(64 * g + ln, kGateWords - 1);
-          const int ri = q / 10, w10 = q % 10;
-          const bool h = (ri & 1) != 0;
-          const int p = j * kPairs + (ri >> 1);
-          const bool routed = p < kI;
-          const int unit = routed ? p : x * kSlice + (p - kI);
-          const bool is_s = w10 < 8;
-          const AIMA_GLOBAL uint8_t* base =
-              is_s ? (routed ? (h ? rs1 : rs0) : (h ? hs1 : hs0))
-                   : (routed ? (h ? rz1 : rz0) : (h ? hz1 : hz0));
-          const uint32_t off = is_s ? (uint32_t)unit * 32 + 4 * w10
-                                    : (uint32_t)unit * 8 + 4 * (w10 - 8);
-          g2[g] = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
+        for (int g = 0; g < 3; ++g) {
+          const int u = min(64 * g + ln, kPairs * 8 - 1);
+          g2[g] = word(uptr(T.gs0) + es, uptr(T.ss0), 32, u);
+          g2[3 + g] = word(uptr(T.gs1) + es, uptr(T.ss1), 32, u);
         }
+        const int uz = min(ln, kPairs * 2 - 1);
+        g2[6] = word(uptr(T.gz0) + ez, uptr(T.sz0), 8, uz);
+        g2[7] = word(uptr(T.gz1) + ez, uptr(T.sz1), 8, uz);
 #pragma unroll
         for (int wv = 0; wv < kWaves; ++wv) {
           const int row = j * kRowsB + wv * kWaveRowsB + (ln >> 4);
@@ -1216,24 +1246,22 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         buf[at + kWaves + g] =
             ld_w(uptr(T.sdq), (uint32_t)x * (kH * 32) + row * 32 + (ln & 1) * 16);
       }
+      // the block's 64 down rows hold 128 consecutive scale words and 32
+      // zero-point words in each of the routed and the shared tensors
       const uint32_t sbytes = (uint32_t)kH * 4 * 2;
       const uint32_t zbytes = (uint32_t)kH * 4 / 2;
-      const AIMA_GLOBAL uint8_t* rs = uptr(T.ds) + (size_t)e * sbytes;
-      const AIMA_GLOBAL uint8_t* rz = uptr(T.dz) + (size_t)e * zbytes;
-      const AIMA_GLOBAL uint8_t* hs = uptr(T.sds);
-      const AIMA_GLOBAL uint8_t* hz = uptr(T.sdz);
-#pragma unroll
-      for (int g = 0; g < 5; ++g) {
-        const int q = 64 * g + ln;  // 320 words: 40 per wave
-        const int wv = q / 40, qq = q % 40;
-        const uint32_t h0 = (uint32_t)(j * kRowsB + wv * kWaveRowsB);
-        const AIMA_GLOBAL uint8_t* base = qq < 16 ? rs : qq < 20 ? rz : qq < 36 ? hs : hz;
-        const uint32_t off = qq < 16   ? h0 * 8 + 4 * qq
-                             : qq < 20 ? h0 * 2 + 4 * (qq - 16)
-                             : qq < 36 ? h0 * 8 + 4 * (qq - 20)
-                                       : h0 * 2 + 4 * (qq - 36);
-        g3[g] = *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(base + off);
-      }
+      const AIMA_GLOBAL uint8_t* rs = uptr(T.ds) + (size_t)e * sbytes + j * kRowsB * 8;
+      const AIMA_GLOBAL uint8_t* hs = uptr(T.sds) + j * kRowsB * 8;
+      const AIMA_GLOBAL uint8_t* rz = uptr(T.dz) + (size_t)e * zbytes + j * kRowsB * 2;
+      const AIMA_GLOBAL uint8_t* hz = uptr(T.sdz) + j * kRowsB * 2;
+      auto ld32 = [](const AIMA_GLOBAL uint8_t* q) {
+        return *reinterpret_cast<const AIMA_GLOBAL uint32_t*>(q);
+      };
+      g3[0] = ld32(rs + 4 * ln);
+      g3[1] = ld32(rs + 256 + 4 * ln);
+      g3[2] = ld32(hs + 4 * ln);
+      g3[3] = ld32(hs + 256 + 4 * ln);
+      g3[4] = ld32((ln < 32 ? rz : hz) + 4 * (ln & 31));
     };
     auto write = [&](int M, int t, int at) {
       const int ln = opaque_v(threadIdx.x & 63);
@@ -1245,16 +1273,16 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       }
       if (t == 2) {
 #pragma unroll
-        for (int g = 0; g < 6; ++g) {
-          const int q = 64 * g + ln;
-          if (q < kGateWords) {
-            const int ri = q / 10, w10 = q % 10;
-            if (w10 < 8) {
-              R.as[ri][w10] = g2[g];
-            } else {
-              R.az[ri][w10 - 8] = g2[g];
-            }
+        for (int g = 0; g < 3; ++g) {
+          const int u = 64 * g + ln;
+          if (u < kPairs * 8) {
+            R.as[u] = g2[g];
+            R.as[kPairs * 8 + u] = g2[3 + g];
           }
+        }
+        if (ln < kPairs * 2) {
+          R.az[ln] = g2[6];
+          R.az[kPairs * 2 + ln] = g2[7];
         }
 #pragma unroll
         for (int wv = 0; wv < kWaves; ++wv) R.b[wv][0][ln] = buf[at + wv];
@@ -1265,10 +1293,8 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
 #pragma unroll
       for (int g = 0; g < 2; ++g) R.bs[4 * g + (ln >> 4)][ln & 15] = buf[at + kWaves + g];
 #pragma unroll
-      for (int g = 0; g < 5; ++g) {
-        const int q = 64 * g + ln;
-        R.bg[q / 40][q % 40] = g3[g];
-      }
+      for (int g = 0; g < 4; ++g) R.bgs[64 * g + ln] = g3[g];
+      R.bgz[ln] = g3[4];
     };
     for (int L = 0; L < a.n_layers; ++L) {
       const int M = L + 1;
@@ -1277,22 +1303,28 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       if (S.abort) return;
       if (L > 0) write(L, 3, 0);
       if (more) issue(M, 0, 0);
+      AIMA_TRACE(L, 26, kWaves * 64);  // batch 3 written, batch 0 issued (stream)
       __syncthreads();  // #2
       if (more) {
         write(M, 0, 0);
         issue(M, 1, 0);
       }
+      AIMA_TRACE(L, 27, kWaves * 64);  // batch 0 written, batch 1 issued (stream)
       __syncthreads();  // #3
+      AIMA_TRACE(L, 21, kWaves * 64);  // #3 passed (stream)
       if (more) {
         write(M, 1, 0);
+        AIMA_TRACE(L, 22, kWaves * 64);  // batch 1 written (stream)
         issue(M, 2, 0);
       }
+      AIMA_TRACE(L, 23, kWaves * 64);  // at #4 (stream)
       __syncthreads();  // #4
       if (S.abort) return;
       if (more) {
         write(M, 2, 0);
         issue(M, 3, 0);
       }
+      AIMA_TRACE(L, 24, kWaves * 64);  // batch 2 written, batch 3 issued (stream)
     }
   };
   if constexpr (RING) {
@@ -1321,15 +1353,23 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
     }
     if (ln < 40) {
       const int ri = ((wave + 4) & 7) + kWaves * (ln >> 3);
-      if (ri < kRowsA) R.as[ri][ln & 7] = gsa_n;
+      if (ri < kRowsA) R.as[(ri & 1) * (kPairs * 8) + (ri >> 1) * 8 + (ln & 7)] = gsa_n;
     } else if (ln < 50) {
       const int ri = ((wave + 4) & 7) + kWaves * ((ln - 40) >> 1);
-      if (ri < kRowsA) R.az[ri][(ln - 40) & 1] = gsa_n;
+      if (ri < kRowsA) R.az[(ri & 1) * (kPairs * 2) + (ri >> 1) * 2 + ((ln - 40) & 1)] = gsa_n;
     }
     R.b[wave][0][ln] = wb_n[0];
     R.b[wave][1][ln] = wb_n[1];
     if (ln < 16) R.bs[wave][ln] = wb_n[2];
-    if (ln < 40) R.bg[wave][ln] = gsb_n;
+    if (ln < 16) {
+      R.bgs[wave * 16 + ln] = gsb_n;
+    } else if (ln < 20) {
+      R.bgz[wave * 4 + ln - 16] = gsb_n;
+    } else if (ln < 36) {
+      R.bgs[kWaves * 16 + wave * 16 + ln - 20] = gsb_n;
+    } else if (ln < 40) {
+      R.bgz[kWaves * 4 + wave * 4 + ln - 36] = gsb_n;
+    }
   }
   AIMA_TRACE(40, 1, 0);  // prologue done
 
@@ -1452,8 +1492,8 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       for (int i = 0; i < kMaxRowsA; ++i) {
         const int ri = min(((wave + 4) & 7) + kWaves * i, kRowsA - 1);
         wa[i] = R.a[ri][ln];
-        sa[i] = R.as[ri][ln >> 3];
-        za[i] = R.az[ri][ln >> 5];
+        sa[i] = R.as[(ri & 1) * (kPairs * 8) + (ri >> 1) * 8 + (ln >> 3)];
+        za[i] = R.az[(ri & 1) * (kPairs * 2) + (ri >> 1) * 2 + (ln >> 5)];
       }
     }
     {
@@ -1464,7 +1504,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         const int e = j * kWaves + wave;
         const int gi = router_row() * gA + ((ln * 32) >> glog2);
         const float lg =
-            segment_sum<64>(u4_chunk_dot(rw, xc, nib(rzw, gi), scl(rsw, gi), magic));
+            segment_sum<64>(lane_dot(rw, xc, nib(rzw, gi), scl(rsw, gi), magic));
         if (lane == 0 && e < a.experts) {
           st_local64(&a.lgx[((size_t)x * 2 + par) * kRouterRows + e], pack_f32(lg, epA));
           if (x == 0 && a.logits_out) a.logits_out[(size_t)L * a.experts + e] = lg;
@@ -1540,6 +1580,9 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         AIMA_TRACE(L, 19, 256);  // gate/up scales in registers (wave 4)
       }
       dots_a(xc, L);
+      AIMA_TRACE(L, 28, 0);    // A dots done (wave 0)
+      AIMA_TRACE(L, 29, 64);   // A dots done (wave 1)
+      AIMA_TRACE(L, 30, 320);  // A dots done (wave 5)
       // routed plan: the layer's down rows once the wave's gate/up rows are
       // consumed.  Issued with the gate/up burst they shared each CU's
       // memory queue with it and delayed the last gate/up row; here they
@@ -1571,15 +1614,21 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
     }
     AIMA_TRACE(L, 4, 0);
     if (wave == 0) {
-      // SwiGLU for the block's 18 pairs, published three per record
-      if (lane < kPairs / 3) {
-        uint64_t rec = (uint64_t)epA << 48;
-#pragma unroll
-        for (int t = 0; t < 3; ++t) {
-          const int lp = 3 * lane + t;
-          rec |= (uint64_t)f2h(silu_mul(S.rowsum[2 * lp], S.rowsum[2 * lp + 1])) << (16 * t);
+      // SwiGLU for the block's 18 pairs, one pair per lane (three pairs per
+      // lane in turn: 0.44 against 0.24-0.32 us from barrier #3 to the
+      // published record; the wave runs alone here), then lane r < 6
+      // publishes pairs 3r .. 3r + 2 as one record
+      {
+        const int lp = min(lane, kPairs - 1);
+        const int hv = (int)f2h(silu_mul(S.rowsum[2 * lp], S.rowsum[2 * lp + 1]));
+        const uint32_t h0 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (3 * lane), hv);
+        const uint32_t h1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (3 * lane + 1), hv);
+        const uint32_t h2 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (3 * lane + 2), hv);
+        if (lane < kPairs / 3) {
+          const uint64_t rec = ((uint64_t)epA << 48) | ((uint64_t)(h2 & 0xffffu) << 32) |
+                               ((h1 & 0xffffu) << 16) | (h0 & 0xffffu);
+          st_local64(&a.actx[((size_t)x * 2 + par) * kActStride + j * (kPairs / 3) + lane], rec);
         }
-        st_local64(&a.actx[((size_t)x * 2 + par) * kActStride + j * (kPairs / 3) + lane], rec);
       }
       AIMA_TRACE(L, 5, 0);  // act published
       // act_L of this XCD: 192 records, lanes read records 2l, 2l+1 and
@@ -1622,6 +1671,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         put_chunk(S.xb_p, S.xb_bias, S.xb_xsum, ln, c);
       }
     }
+    AIMA_TRACE(L, 25, 0);  // at #4 (wave 0)
     __syncthreads();  // #4: act_L operands staged
     AIMA_TRACE(L, 7, 0);
     if (S.abort) {
@@ -1648,12 +1698,12 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int r = 4 * u + (ln >> 4);
-        sb[u] = R.bg[wave][2 * r + ((ln & 15) >> 3)];
-        zb[u] = R.bg[wave][16 + (r >> 1)];
+        sb[u] = R.bgs[wave * 16 + 2 * r + ((ln & 15) >> 3)];
+        zb[u] = R.bgz[wave * 4 + (r >> 1)];
       }
       const int r8 = (ln & 15) >> 1;
-      sb[2] = R.bg[wave][20 + 2 * r8 + (x >> 2)];
-      zb[2] = R.bg[wave][36 + (r8 >> 1)];
+      sb[2] = R.bgs[kWaves * 16 + wave * 16 + 2 * r8 + (x >> 2)];
+      zb[2] = R.bgz[kWaves * 4 + wave * 4 + (r8 >> 1)];
     }
     // ================= phase B_L =================
     {
@@ -1666,7 +1716,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         get_chunk(S.xb_p, S.xb_bias, S.xb_xsum, cl, xc);
         const int row = h0 + 4 * u + (ln >> 4);
         const int gi = row * gB + ((cl * 32) >> glog2);
-        dr[u] = segment_sum<16>(u4_chunk_dot(wb[u], xc, nib(zb[u], gi), scl(sb[u], gi), magic));
+        dr[u] = segment_sum<16>(lane_dot(wb[u], xc, nib(zb[u], gi), scl(sb[u], gi), magic));
       }
       float ds;
       {
@@ -1675,7 +1725,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         const int row = h0 + ((ln & 15) >> 1);
         const int ch = 2 * x + (ln & 1);
         const int gi = row * gB + ((ch * 32) >> glog2);
-        ds = segment_sum<2>(u4_chunk_dot(wb[2], xc, nib(zb[2], gi), scl(sb[2], gi), magic));
+        ds = segment_sum<2>(lane_dot(wb[2], xc, nib(zb[2], gi), scl(sb[2], gi), magic));
       }
       // lane r < 8 gathers row r: routed sum from lane 16 (r & 3) of unit
       // r >> 2, shared sum from lane 2r

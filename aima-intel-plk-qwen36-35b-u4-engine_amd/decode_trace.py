@@ -57,6 +57,18 @@ ROUTED_PHASES = [(0, 1, "r_L read -> barrier #1"),
                  (7, 8, "#4 -> P published (down dots)"),
                  (8, 9, "P published -> P read (cross-XCD hop)"),
                  (9, 10, "P read -> r_{L+1} rows stored (relay)")]
+# the streaming wave of the weight-ring instance (logits-fed plan) against
+# the compute waves' barriers
+RING_PHASES = [(2, 28, "#2 -> gate/up dots done (wave 0)"),
+               (2, 29, "#2 -> gate/up dots done (wave 1)"),
+               (2, 30, "#2 -> gate/up dots done (wave 5)"),
+               (1, 26, "#1 -> stream: batch 3 written, 0 issued"),
+               (2, 27, "#2 -> stream: batch 0 written, 1 issued"),
+               (21, 22, "stream: #3 -> batch 1 written"),
+               (22, 23, "stream: batch 1 written -> at #4"),
+               (25, 7, "wave 0 at #4 -> #4 passed"),
+               (23, 7, "stream at #4 -> #4 passed"),
+               (7, 24, "#4 -> stream: batch 2 written, 3 issued")]
 
 
 def main():
@@ -114,6 +126,14 @@ def main():
     for a0, a1, name in phases:
         print("%-44s %s" % (name, st(np.concatenate([A[l][:, a1] - A[l][:, a0]
                                                      for l in range(2, 38)]))))
+    if not args.routed:
+        simd = raw[40, :, 16:25]
+        maps, counts = np.unique(simd, axis=0, return_counts=True)
+        for m, c in sorted(zip(maps.tolist(), counts.tolist()), key=lambda t: -t[1])[:3]:
+            print("SIMD of waves 0..8 (last: the streaming wave): %s in %d blocks" % (m, c))
+        for a0, a1, name in RING_PHASES:
+            print("%-44s %s" % (name, st(np.concatenate([A[l][:, a1] - A[l][:, a0]
+                                                         for l in range(2, 38)]))))
     hop = [A[l, :, 0] - A[l - 1, :, 10].max() for l in range(2, 38)]
     print("%-44s %s" % ("last r_L store -> r_L read (residual hop)", st(np.concatenate(hop))))
     # The hops measured from the last stamp a reader depends on (block b is
