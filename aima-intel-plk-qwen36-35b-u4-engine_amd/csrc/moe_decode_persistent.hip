@@ -225,6 +225,16 @@ __device__ __forceinline__ float lane_dot(const u32x4 w, const XChunk& c, uint32
   return t;
 }
 
+// f32 -> f16 of a value rounded to f32 first, as the arithmetic reads (and
+// as the CPU reference converts): without the empty asm the compiler may
+// fold the final multiply or add into a mixed-precision FMA that rounds once
+// to f16, or not, depending on the surrounding code -- rare one-ulp
+// differences between the kernel's instances.
+__device__ __forceinline__ uint16_t f2h_rounded(float f) {
+  asm volatile("" : "+v"(f));
+  return f2h(f);
+}
+
 __device__ __forceinline__ uint64_t pack_f32(float v, uint32_t epoch) {
   return (uint64_t)__builtin_bit_cast(uint32_t, v) | ((uint64_t)epoch << 32);
 }
@@ -1446,7 +1456,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       const float scale = 1.0f / sqrtf(sst / (float)kH + a.eps);
       uint16_t xh[4];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) xh[t] = f2h(rf[t] * scale * as_f32(nw[t]));
+      for (int t = 0; t < 4; ++t) xh[t] = f2h_rounded(rf[t] * scale * as_f32(nw[t]));
       const uint32_t X0 = (uint32_t)xh[0] | ((uint32_t)xh[1] << 16);
       const uint32_t X1 = (uint32_t)xh[2] | ((uint32_t)xh[3] << 16);
       // partner lane (l ^ 1) holds the other half of the 8-value word group
@@ -1620,7 +1630,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       // publishes pairs 3r .. 3r + 2 as one record
       {
         const int lp = min(lane, kPairs - 1);
-        const int hv = (int)f2h(silu_mul(S.rowsum[2 * lp], S.rowsum[2 * lp + 1]));
+        const int hv = (int)f2h_rounded(silu_mul(S.rowsum[2 * lp], S.rowsum[2 * lp + 1]));
         const uint32_t h0 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (3 * lane), hv);
         const uint32_t h1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (3 * lane + 1), hv);
         const uint32_t h2 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (3 * lane + 2), hv);
@@ -1771,7 +1781,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       for (int q = 0; q < kXcds; ++q) f += as_f32((uint32_t)v[q]);
       const int h = j * kRowsB + ln;
       const uint16_t rh = (uint16_t)(S.rl[h >> 1] >> ((h & 1) * 16));
-      const uint16_t o = f2h(h2f(rh) + f);
+      const uint16_t o = f2h_rounded(h2f(rh) + f);
       if (!have) {
         // nothing is published after a timeout
       } else if (L + 1 < a.n_layers) {

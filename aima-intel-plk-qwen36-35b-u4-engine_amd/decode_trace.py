@@ -62,6 +62,7 @@ ROUTED_PHASES = [(0, 1, "r_L read -> barrier #1"),
 RING_PHASES = [(2, 28, "#2 -> gate/up dots done (wave 0)"),
                (2, 29, "#2 -> gate/up dots done (wave 1)"),
                (2, 30, "#2 -> gate/up dots done (wave 5)"),
+               (2, 3, "#2 -> gate/up dots done (wave 4)"),
                (1, 26, "#1 -> stream: batch 3 written, 0 issued"),
                (2, 27, "#2 -> stream: batch 0 written, 1 issued"),
                (21, 22, "stream: #3 -> batch 1 written"),
@@ -127,10 +128,10 @@ def main():
         print("%-44s %s" % (name, st(np.concatenate([A[l][:, a1] - A[l][:, a0]
                                                      for l in range(2, 38)]))))
     if not args.routed:
-        simd = raw[40, :, 16:25]
+        simd = raw[40, :, 16:29]
         maps, counts = np.unique(simd, axis=0, return_counts=True)
         for m, c in sorted(zip(maps.tolist(), counts.tolist()), key=lambda t: -t[1])[:3]:
-            print("SIMD of waves 0..8 (last: the streaming wave): %s in %d blocks" % (m, c))
+            print("SIMD of waves 0..12 (last: the streaming wave): %s in %d blocks" % (m, c))
         for a0, a1, name in RING_PHASES:
             print("%-44s %s" % (name, st(np.concatenate([A[l][:, a1] - A[l][:, a0]
                                                          for l in range(2, 38)]))))
