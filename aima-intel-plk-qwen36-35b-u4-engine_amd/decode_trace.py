@@ -128,10 +128,10 @@ def main():
         print("%-44s %s" % (name, st(np.concatenate([A[l][:, a1] - A[l][:, a0]
                                                      for l in range(2, 38)]))))
     if not args.routed:
-        simd = raw[40, :, 16:29]
+        simd = raw[40, :, 16:25]
         maps, counts = np.unique(simd, axis=0, return_counts=True)
         for m, c in sorted(zip(maps.tolist(), counts.tolist()), key=lambda t: -t[1])[:3]:
-            print("SIMD of waves 0..12 (last: the streaming wave): %s in %d blocks" % (m, c))
+            print("SIMD of waves 0..8 (last: the streaming wave): %s in %d blocks" % (m, c))
         for a0, a1, name in RING_PHASES:
             print("%-44s %s" % (name, st(np.concatenate([A[l][:, a1] - A[l][:, a0]
                                                          for l in range(2, 38)]))))
