@@ -250,7 +250,9 @@ struct SharedState {
   alignas(16) uint32_t rl[kH / 2];      // r_L, f16 pairs (read by the relay)
   float ss[kWaves];                    // per-wave sums of squares of r_L
   float gp[kWaves];                    // per-wave shared-gate partial dots
-  float rowsum[kRowsA];
+  // gate/up row sums as four 16-lane partials (lanes 0-15, 16-31, 32-47,
+  // 48-63), summed (p0 + p1) + (p2 + p3) where used: segment_sum<64>'s order
+  alignas(16) float rowpart[kRowsA][4];
   PlanLayer table[kMaxLayers];         // the layer table, copied once
   int32_t route_id[kMaxLayers][kMaxK];
   float route_w[kMaxLayers][kMaxK];
@@ -1163,8 +1165,8 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
         const int unit = p < kI ? p : x * kSlice + (p - kI);
         const int gi = unit * gA + ((ln * 32) >> glog2);
         const float dd =
-            segment_sum<64>(lane_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
-        if ((threadIdx.x & 63) == 0 && ri < kRowsA) S.rowsum[ri] = dd;
+            segment_sum<16>(lane_dot(wa[i], xc, nib(za[i], gi), scl(sa[i], gi), magic));
+        if ((ln & 15) == 0 && ri < kRowsA) S.rowpart[ri][ln >> 4] = dd;
       }
     }
   };
@@ -1630,7 +1632,11 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       // publishes pairs 3r .. 3r + 2 as one record
       {
         const int lp = min(lane, kPairs - 1);
-        const int hv = (int)f2h_rounded(silu_mul(S.rowsum[2 * lp], S.rowsum[2 * lp + 1]));
+        auto row_total = [&](int ri) {
+          const float4 q = *reinterpret_cast<const float4*>(&S.rowpart[ri][0]);
+          return (q.x + q.y) + (q.z + q.w);
+        };
+        const int hv = (int)f2h_rounded(silu_mul(row_total(2 * lp), row_total(2 * lp + 1)));
         const uint32_t h0 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (3 * lane), hv);
         const uint32_t h1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (3 * lane + 1), hv);
         const uint32_t h2 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (3 * lane + 2), hv);
