@@ -1314,11 +1314,13 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       __syncthreads();  // #1
       if (S.abort) return;
       if (L > 0) write(L, 3, 0);
+      AIMA_TRACE(L, 13, kWaves * 64);  // batch 3 written (stream)
       if (more) issue(M, 0, 0);
       AIMA_TRACE(L, 26, kWaves * 64);  // batch 3 written, batch 0 issued (stream)
       __syncthreads();  // #2
       if (more) {
         write(M, 0, 0);
+        AIMA_TRACE(L, 17, kWaves * 64);  // batch 0 written (stream)
         issue(M, 1, 0);
       }
       AIMA_TRACE(L, 27, kWaves * 64);  // batch 0 written, batch 1 issued (stream)
@@ -1431,6 +1433,7 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
     if (lane == 0) S.ss[wave] = ss;
     *reinterpret_cast<u32x2*>(&S.rl[wave * 128 + ln * 2]) =
         u32x2{(rv[0] & 0xffffu) | (rv[1] << 16), (rv[2] & 0xffffu) | (rv[3] << 16)};
+    if (!ROUTED) AIMA_TRACE(L, 14, 0);  // at #1 (wave 0)
     __syncthreads();  // #1: r_L sums of squares
     AIMA_TRACE(L, 1, 0);
     if (S.abort) {
@@ -1490,6 +1493,10 @@ __global__ __launch_bounds__(RING ? kRingThreads : kThreads, 1) void decode_pers
       g += (float)g1.y * h2f(xh[3]);
       g = segment_sum<64>(g);
       if (lane == 0) S.gp[wave] = g;
+    }
+    if (!ROUTED) {
+      AIMA_TRACE(L, 11, 0);    // at #2 (wave 0)
+      AIMA_TRACE(L, 12, 256);  // at #2 (wave 4)
     }
     __syncthreads();  // #2: A operands ready
     AIMA_TRACE(L, 2, 0);

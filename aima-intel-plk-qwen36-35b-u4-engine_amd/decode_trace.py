@@ -63,7 +63,13 @@ RING_PHASES = [(2, 28, "#2 -> gate/up dots done (wave 0)"),
                (2, 29, "#2 -> gate/up dots done (wave 1)"),
                (2, 30, "#2 -> gate/up dots done (wave 5)"),
                (2, 3, "#2 -> gate/up dots done (wave 4)"),
+               (14, 1, "wave 0 at #1 -> #1 passed"),
+               (1, 11, "#1 -> wave 0 at #2"),
+               (1, 12, "#1 -> wave 4 at #2"),
+               (1, 13, "#1 -> stream: batch 3 written"),
                (1, 26, "#1 -> stream: batch 3 written, 0 issued"),
+               (11, 2, "wave 0 at #2 -> #2 passed"),
+               (2, 17, "#2 -> stream: batch 0 written"),
                (2, 27, "#2 -> stream: batch 0 written, 1 issued"),
                (21, 22, "stream: #3 -> batch 1 written"),
                (22, 23, "stream: batch 1 written -> at #4"),
@@ -135,6 +141,8 @@ def main():
         for a0, a1, name in RING_PHASES:
             print("%-44s %s" % (name, st(np.concatenate([A[l][:, a1] - A[l][:, a0]
                                                          for l in range(2, 38)]))))
+        print("%-44s %s" % ("stream at #1 -> #1 passed", st(np.concatenate(
+            [A[l][:, 1] - A[l - 1][:, 24] for l in range(2, 38)]))))
     hop = [A[l, :, 0] - A[l - 1, :, 10].max() for l in range(2, 38)]
     print("%-44s %s" % ("last r_L store -> r_L read (residual hop)", st(np.concatenate(hop))))
     # The hops measured from the last stamp a reader depends on (block b is
