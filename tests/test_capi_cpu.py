@@ -268,6 +268,53 @@ def test_prefill_workspace_views(pkg):
     assert base <= v.tile_count < v.offsets
 
 
+def _tiles_needed(counts, T, bm=256):
+    """Tile records the schedule writes: per expert with rows, its full 256-row
+    tiles and one remainder tile; the shared expert's T rows likewise."""
+    n = sum(c // bm + (1 if c % bm else 0) for c in counts)
+    return n + T // bm + (1 if T % bm else 0)
+
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 256), (7, 8, 256), (2048, 8, 256), (300, 16, 1024),
+                                   (16384, 8, 256), (33, 1, 4)])
+def test_prefill_workspace_holds_every_tile(pkg, T, k, E):
+    """The tile array of the prefill workspace (carved by the library's own
+    layout, read back through aima_moe_prefill_workspace_views) has room for
+    the tile records of any routing: uniform, concentrated on k experts,
+    spread one row per expert, and Zipf-skewed, with the group sizes taken
+    from the oracle's schedule (the checker)."""
+    import numpy as np
+
+    import oracle
+
+    L = pkg._lib
+    lc = _fake_layer(pkg, E=E)
+    size = L.size_query("aima_moe_prefill_workspace_size", C.byref(lc), T, k)
+    base = 1 << 30
+    v = L.PrefillViewsC()
+    L.call("aima_moe_prefill_workspace_views", C.byref(lc), T, k, C.c_void_p(base), C.byref(v))
+    capacity = (v.token_map - v.tiles) // 16
+    assert base + size >= v.contributions + (T * k + T) * 2048 * 2
+    rng = np.random.default_rng(T * 31 + k * 7 + E)
+    zipf = 1.0 / np.arange(1, E + 1) ** 1.1
+    routings = {
+        "uniform": np.stack([rng.permutation(E)[:k] for _ in range(T)]),
+        "concentrated": np.tile(np.arange(k), (T, 1)),
+        "spread": np.arange(T * k).reshape(T, k) % E,
+        "zipf": np.stack([rng.choice(E, size=k, replace=False, p=zipf / zipf.sum())
+                          for _ in range(T)]),
+    }
+    for name, ids in routings.items():
+        ids = ids.astype(np.int32)
+        assert all(len(set(r)) == k for r in ids.tolist())  # no expert twice per token
+        s = oracle.build_grouped_schedule(ids, E)
+        ends = s["offsets"].astype(np.int64)
+        counts = np.diff(np.concatenate([[0], ends]))
+        assert counts.sum() == T * k
+        need = _tiles_needed(counts.tolist(), T)
+        assert need <= capacity, (name, need, capacity)
+
+
 def test_dequant_f16_validation(pkg):
     L = pkg._lib
     lib = L.lib()
