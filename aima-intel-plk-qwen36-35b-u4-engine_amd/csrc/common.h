@@ -315,22 +315,8 @@ __device__ __forceinline__ f16x8 dequant8(uint32_t d, f16x2 zz2, f16x2 ss2, uint
 // global address space.
 #define AIMA_GLOBAL __attribute__((address_space(1)))
 
-__device__ __forceinline__ u32x4 gload16_nt(const void* p) {
-  return __builtin_nontemporal_load((const AIMA_GLOBAL u32x4*)(p));
-}
-__device__ __forceinline__ float gload_h2f(const uint16_t* p, int64_t i) {
-  return h2f(((const AIMA_GLOBAL uint16_t*)(p))[i]);
-}
-__device__ __forceinline__ uint32_t gload_u4(const uint8_t* packed, int64_t i) {
-  const uint32_t b = ((const AIMA_GLOBAL uint8_t*)(packed))[i >> 1];
-  return (i & 1) ? (b >> 4) : (b & 0x0fu);
-}
 __device__ __forceinline__ u32x4 gload16(const void* p) {
   return *((const AIMA_GLOBAL u32x4*)(p));
-}
-
-__device__ __forceinline__ u32x4 load16(const void* p) {
-  return *reinterpret_cast<const u32x4*>(p);
 }
 
 __device__ __forceinline__ u32x4 load16_nt(const void* p) {
